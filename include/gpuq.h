@@ -1,0 +1,87 @@
+/* include/gpuq.h - C ABI of libgpuq.so, the GGUF quantizer for AMD Instinct MI355X (gfx950).
+ *
+ * The first twelve entry points are the reference library's own (zephel01/trench-gguf gpuq/gpuq.hip), with the
+ * same signatures, ggml type ids, return conventions and gpuq_tables.bin format, so the reference's ctypes callers
+ * (tools/requant_experts.py, tools/convert_hf.py, tools/requant_table.py, tools/ldlq.py) load this library
+ * unchanged. Each cites the reference function it replaces. The entry points after them are additions.
+ *
+ * Conventions (as the reference's):
+ *   - ggml type ids: Q8_0 8, Q2_K 10, Q3_K 11, Q4_K 12, Q5_K 13, Q6_K 14, IQ2_XXS 16, IQ2_XS 17, IQ3_XXS 18,
+ *     IQ1_S 19, IQ4_NL 20, IQ3_S 21, IQ2_S 22, IQ4_XS 23, IQ1_M 29; sources F32 0, F16 1, Q8_0 8, BF16 30, MXFP4 39.
+ *   - Host entry points take host pointers, are synchronous and return the bytes written, 0 on any error.
+ *   - Device entry points (*_dev) take device pointers, enqueue on `stream` (a hipStream_t, NULL = the null
+ *     stream) without synchronizing, and return the bytes the launch will write, 0 on error.
+ *   - Output is the ggml block layout, byte-identical to ggml_quantize_chunk / to_float for the same tables.
+ *   - The library keeps process-global staging buffers and tables: calls are serialized internally; the device is
+ *     the one passed to gpuq_init.
+ */
+#ifndef GPUQ_H
+#define GPUQ_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* gpuq/gpuq.hip:2059 gpuq_init. Selects the device and loads the search / dequantizer tables. 0 ok; 1 no such
+ * device; 2 cannot open the file; 3 short or malformed record; 4 device allocation failed; 6 a table fails the
+ * consistency checks (a point whose key does not map back to it, or a reachable key with no candidate). A file with
+ * no records returns 0 (the k-quants, Q8_0 and IQ4 need no tables). */
+int gpuq_init(const char *tables_path, int device);
+
+/* gpuq/gpuq.hip:2082 gpuq_block_bytes: bytes of one block of the type, 0 for an unknown type */
+size_t gpuq_block_bytes(int type);
+
+/* gpuq/gpuq.hip:2213 gpuq_can_quantize: 1 when gpuq_quantize* takes the type with (1) or without (0) an imatrix */
+int gpuq_can_quantize(int type, int with_imatrix);
+
+/* gpuq/gpuq.hip:2228 gpuq_quantize: nrow x n_per_row f32 (host) -> dst (host), imatrix: n_per_row weights or NULL */
+size_t gpuq_quantize(int type, const float *src, void *dst, int64_t nrow, int64_t n_per_row, const float *imatrix);
+
+/* gpuq/gpuq.hip:2219 gpuq_quantize_batch: nmat matrices, matrix m weighted by imatrix row m (nmat x n_per_row) */
+size_t gpuq_quantize_batch(int type, const float *src, void *dst, int64_t nmat, int64_t nrow, int64_t n_per_row,
+                           const float *imatrix);
+
+/* gpuq/gpuq.hip:2235 gpuq_can_dequantize: 1 when gpuq_requantize* reads this source type */
+int gpuq_can_dequantize(int src_type);
+
+/* gpuq/gpuq.hip:2252 gpuq_requantize: source bytes (host, type src) -> decoded on the GPU -> quantized -> dst */
+size_t gpuq_requantize(int src_type, const void *raw, int type, void *dst, int64_t nrow, int64_t n_per_row,
+                       const float *imatrix);
+
+/* gpuq/gpuq.hip:2239 gpuq_requantize_batch */
+size_t gpuq_requantize_batch(int src_type, const void *raw, int type, void *dst, int64_t nmat, int64_t nrow,
+                             int64_t n_per_row, const float *imatrix);
+
+/* gpuq/gpuq.hip:2283 gpuq_quantize_dev: nblocks 256-weight super-blocks of d_x -> d_dst, block b weighted by
+ * d_qw + ((b % qw_mod) / qw_div) * 256. Takes every 256-block type (the reference: the i-quants and IQ4_XS).
+ * d_x and d_qw 16-byte aligned. */
+size_t gpuq_quantize_dev(int type, const float *d_x, void *d_dst, int64_t nblocks, const float *d_qw, int64_t qw_mod,
+                         int64_t qw_div, void *stream);
+
+/* gpuq/gpuq.hip:2292 gpuq_can_dequantize_type: 1 for the i-quants with a dequantizer grid, and IQ4_XS */
+int gpuq_can_dequantize_type(int type);
+
+/* gpuq/gpuq.hip:2302 gpuq_dequantize_dev: nblocks blocks (device) -> nblocks*256 f32 (device), ggml's to_float */
+size_t gpuq_dequantize_dev(int type, const void *d_q, float *d_out, int64_t nblocks, void *stream);
+
+/* gpuq/gpuq.hip:2323 gpuq_dequantize_src_dev: n values (n % 32 == 0) of F32/F16/BF16/Q8_0/MXFP4 bytes -> f32 */
+size_t gpuq_dequantize_src_dev(int src_type, const void *d_raw, float *d_out, int64_t n, void *stream);
+
+/* ---- additions (no counterpart in the reference) ---- */
+
+/* Device-resident requantize: nmat matrices of nrow x n_per_row values stored as src_type (F32, BF16 or MXFP4,
+ * decoded in registers inside the quantize kernel) -> d_dst, matrix m weighted by d_imatrix + m*n_per_row (or
+ * none). For callers that keep the source in HBM (the streaming driver, the benchmark). */
+size_t gpuq_requantize_dev(int src_type, const void *d_raw, int type, void *d_dst, int64_t nmat, int64_t nrow,
+                           int64_t n_per_row, const float *d_imatrix, void *stream);
+
+/* Reads and clears the flag the kernels set where the reference would trap (a key with no candidate point: non-
+ * finite input or an inconsistent table). Synchronizes the device. */
+int gpuq_take_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

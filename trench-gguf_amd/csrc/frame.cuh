@@ -1,0 +1,119 @@
+// trench-gguf_amd/csrc/frame.cuh - the launch frame shared by the super-block quantizers.
+//
+// Work decomposition (gfx950, wave64): a super-block of 256 weights is owned by G consecutive lanes (G = 8 for the
+// 32-weight sub-block types, 16 for the 16-weight ones), lane g holding sub-block g's weights, importances and
+// search state in registers. The per-sub-block searches of ggml run on their lane in ggml's own serial order, so no
+// cross-lane arithmetic reorders a sum; the few super-block-wide quantities are lane-to-lane chains (sums) or
+// order-free reductions (max). A wave therefore quantizes 64/G super-blocks at once, with 100% lane occupancy in the
+// fixed-trip-count search loops. Each wave assembles its super-blocks' output bytes in an LDS image and writes them
+// to HBM as one contiguous, dword-coalesced range. Workgroups of 4 waves loop over the super-blocks (grid-stride),
+// so the per-workgroup LDS table staging of the i-quants is paid once per workgroup.
+#pragma once
+#include "common.cuh"
+
+#define WG_THREADS 256
+#define WG_WAVES 4
+
+struct QParams {
+    const uint8_t *src;     // source tensor bytes (type SRC), super-block b at element b*QK
+    const float *qw;        // importance rows or nullptr
+    int64_t qw_mat, qw_mod, qw_div;   // block b reads row (b / qw_mat) * qw_mod + (b % qw_mod) / qw_div
+    uint8_t *dst;           // output blocks
+    int64_t nsb;            // units: super-blocks, or 32-blocks for Q8_0 / IQ4_NL
+    // i-quant tables (device): search grid, full 2-bit / 3-bit key map, ggml-layout neighbour lists, and for the
+    // 8-value types the map re-indexed by base-3 keys (levels 0..2), staged into LDS by the kernels
+    const uint64_t *grid;
+    const int32_t *map;
+    const uint16_t *neigh;
+    const int32_t *map3;
+    int grid_size, map_size, neigh_len;
+    int *err;               // set when a search finds no candidate (the reference traps there)
+};
+
+DEV int64_t qw_row(const QParams &p, int64_t b) { return (b / p.qw_mat) * p.qw_mod + (b % p.qw_mod) / p.qw_div; }
+
+template <int N> DEV void load_qw(const float *row, float (&w)[N]) {
+    const float4 *p = (const float4 *)row;
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+        const float4 q = p[i];
+        w[4 * i + 0] = q.x; w[4 * i + 1] = q.y; w[4 * i + 2] = q.z; w[4 * i + 3] = q.w;
+    }
+}
+
+// ------------------------------------------------------------------ the LDS block image
+// Bytes are combined with LDS atomic ORs on the containing dword, so fields that several lanes fill (shared high
+// bits, packed nibbles) need no ordering between lanes. The image is zeroed before every tile. `img` is the wave's
+// 16-byte aligned image and `off` a byte offset in it (a block's fields sit at blk_off + field offset).
+DEV void img_or8(uint8_t *img, int off, uint32_t v) {
+    atomicOr((unsigned int *)(img + (off & ~3)), (v & 0xffu) << (8 * (off & 3)));
+}
+DEV void img_or16(uint8_t *img, int off, uint32_t v) {   // off even
+    atomicOr((unsigned int *)(img + (off & ~3)), (v & 0xffffu) << (8 * (off & 3)));
+}
+DEV void img_or32(uint8_t *img, int off, uint32_t v) {   // off even
+    if ((off & 3) == 0) atomicOr((unsigned int *)(img + off), v);
+    else { img_or16(img, off, v & 0xffffu); img_or16(img, off + 2, v >> 16); }
+}
+
+DEV void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
+DEV void img_zero(uint8_t *img, int nbytes) {
+    for (int i = lane_id() * 4; i < nbytes; i += 64 * 4) *(uint32_t *)(img + i) = 0u;
+}
+
+// copy nbytes (even) of the image to global dst (2-byte aligned) with coalesced dword stores
+DEV void img_store(uint8_t *dst, const uint8_t *img, int nbytes) {
+    const int lane = lane_id();
+    int head = ((uintptr_t)dst & 3) ? 2 : 0;            // dst is at least 2-byte aligned
+    if (head > nbytes) head = nbytes;
+    if (head && lane == 0) *(uint16_t *)dst = *(const uint16_t *)img;
+    const int nw = (nbytes - head) / 4;
+    for (int i = lane; i < nw; i += 64) {
+        const uint8_t *s = img + head + 4 * i;
+        uint32_t v;
+        if (head) v = (uint32_t)*(const uint16_t *)s | ((uint32_t)*(const uint16_t *)(s + 2) << 16);
+        else v = *(const uint32_t *)s;
+        *(uint32_t *)(dst + head + 4 * i) = v;
+    }
+    const int tail = nbytes - head - 4 * nw;             // 0 or 2
+    if (tail && lane == 0) *(uint16_t *)(dst + nbytes - 2) = *(const uint16_t *)(img + nbytes - 2);
+}
+
+// ------------------------------------------------------------------ the kernel
+// T provides: BS (weights a unit: 256, or 32 for Q8_0 / IQ4_NL), G (lanes a unit), N (= BS / G), BB (unit bytes),
+// TAB (LDS table bytes, 0 for none),
+// stage(p, lds) (cooperative table staging, before the barrier), and
+// quant(x, qw, g, img, boff, lds, p): lane g's part of one super-block, OR-ing its bytes into img at boff.
+template <class T> constexpr int img_bytes() { return ((64 / T::G) * T::BB + 15) & ~15; }
+
+template <class T, int SRC>
+__global__ __launch_bounds__(WG_THREADS) void k_quant(QParams p) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr int SPW = 64 / T::G;
+    if (T::TAB) {
+        T::stage(p, lds);
+        __syncthreads();
+    }
+    const int wave = (int)(threadIdx.x >> 6), lane = lane_id();
+    const int g = lane % T::G, slot = lane / T::G;
+    uint8_t *img = lds + T::TAB + wave * img_bytes<T>();
+    const int64_t nwaves = (int64_t)gridDim.x * WG_WAVES;
+    for (int64_t t = (int64_t)blockIdx.x * WG_WAVES + wave; t * SPW < p.nsb; t += nwaves) {
+        const int64_t b0 = t * SPW;
+        const int nact = (int)(p.nsb - b0 < SPW ? p.nsb - b0 : SPW);
+        const int64_t b = b0 + (slot < nact ? slot : nact - 1);
+        img_zero(img, img_bytes<T>());
+        wave_sync();
+        float x[T::N];
+        SrcLoad<SRC, T::N>::load(p.src, b * T::BS + g * T::N, x);
+        const float *qw = p.qw ? p.qw + qw_row(p, b) * T::BS + g * T::N : nullptr;
+        T::quant(x, qw, g, img, slot * T::BB, lds, p);
+        wave_sync();
+        img_store(p.dst + b0 * T::BB, img, nact * T::BB);
+        wave_sync();
+    }
+}

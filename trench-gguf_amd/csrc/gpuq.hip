@@ -1,0 +1,465 @@
+// trench-gguf_amd/csrc/gpuq.hip - libgpuq.so: the GGUF quantizer for MI355X (gfx950), C ABI.
+//
+// Build: hipcc -O3 -ffp-contract=off -fno-fast-math --offload-arch=gfx950 -fPIC -shared (see the package Makefile).
+// The exported functions keep the reference library's signatures, return conventions and table file format
+// (gpuq/gpuq.hip:2059-2328 of the reference), so its Python drivers load this library unchanged; they are declared
+// with their reference counterparts in include/gpuq.h.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "common.cuh"
+#include "frame.cuh"
+#include "kquants.cuh"
+#include "iq2.cuh"
+#include "iq1.cuh"
+#include "iq3.cuh"
+#include "dequant.cuh"
+
+extern "C" size_t gpuq_block_bytes(int type);
+
+namespace {
+
+struct Tabs {
+    bool ok = false;
+    uint64_t *grid = nullptr;   // search grid
+    int32_t *map = nullptr;     // full key map (2-bit keys, 43692; 3-bit keys, 4096)
+    int32_t *map3 = nullptr;    // 8-value types: the map re-indexed by base-3 keys (6561)
+    uint16_t *neigh = nullptr;
+    int grid_size = 0, map_size = 0, neigh_len = 0;
+    uint64_t *dq = nullptr;     // dequantizer grid (record 1000 + type)
+    int dq_size = 0;
+};
+
+Tabs g_tabs[64];
+int g_device = -1;
+int g_ncu = 256;
+int *g_err = nullptr;          // device flag: a search found no candidate (the reference traps there)
+std::mutex g_mu;               // the host API's staging buffers are process-global
+
+struct Buf {
+    void *p = nullptr;
+    size_t cap = 0;
+    bool grow(size_t need) {
+        if (need <= cap) return true;
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        cap = 0;
+        if (hipMalloc(&p, need) != hipSuccess) return false;
+        cap = need;
+        return true;
+    }
+};
+Buf g_raw, g_qw, g_out, g_f32;
+
+bool is_search_type(int t) {
+    return t == T_IQ2_XXS || t == T_IQ2_XS || t == T_IQ2_S || t == T_IQ1_S || t == T_IQ3_XXS || t == T_IQ3_S;
+}
+int expected_grid(int t) {
+    switch (t) {
+        case T_IQ2_XXS: return 256;
+        case T_IQ2_XS: return 512;
+        case T_IQ2_S: return 1024;
+        case T_IQ1_S: return 2048;
+        case T_IQ3_XXS: return 256;
+        case T_IQ3_S: return 512;
+        default: return 0;
+    }
+}
+bool eight_values(int t) { return t != T_IQ3_XXS && t != T_IQ3_S; }
+
+// search tables of a type: IQ1_M searches IQ1_S's (gpuq/gpuq.hip:2051-2056)
+const Tabs &tab_of(int type) { return g_tabs[type == T_IQ1_M ? T_IQ1_S : type]; }
+
+// The checks that make the LDS layout exact: every point's key is in the map and maps back to the point, and every
+// key the trial rounding can produce is on the grid or has a non-empty, in-range neighbour list.
+bool valid_search(int t, const std::vector<uint64_t> &grid, const std::vector<int32_t> &map,
+                  const std::vector<uint16_t> &neigh) {
+    const bool e8 = eight_values(t);
+    const int nv = e8 ? 8 : 4, bits = e8 ? 2 : 3, maxlev = e8 ? 3 : 7;
+    if ((int)grid.size() != expected_grid(t) || (int)map.size() != (e8 ? 43692 : 4096)) return false;
+    const int G = (int)grid.size(), M = (int)map.size(), NL = (int)neigh.size();
+    for (int g = 0; g < G; ++g) {
+        int u = 0;
+        for (int i = 0; i < nv; ++i) {
+            const int b = (int)((grid[g] >> (8 * i)) & 0xff);
+            if (b < 1 || b > 2 * maxlev + 1 || !(b & 1)) return false;
+            u |= ((b - 1) / 2) << (bits * i);
+        }
+        if (e8 && ((grid[g] >> 0) >> 63)) return false;
+        if (!e8 && (grid[g] >> 32)) return false;
+        if (u >= M || map[u] != g) return false;
+    }
+    const int nkeys = e8 ? 6561 : 4096;
+    for (int k = 0; k < nkeys; ++k) {
+        int u = k;
+        if (e8) {
+            u = 0;
+            int r = k;
+            for (int i = 0; i < 8; ++i) { u |= (r % 3) << (2 * i); r /= 3; }
+        }
+        const int m = map[u];
+        if (m >= 0) {
+            if (m >= G) return false;
+            continue;
+        }
+        const int64_t off = -(int64_t)m - 1;
+        if (off >= NL) return false;
+        const int cnt = neigh[off];
+        if (cnt < 1 || off + cnt >= NL) return false;
+        for (int j = 1; j <= cnt; ++j)
+            if (neigh[off + j] >= G) return false;
+    }
+    return true;
+}
+
+template <class V> bool upload(V **dst, const std::vector<V> &src) {
+    if (src.empty()) return true;
+    if (hipMalloc((void **)dst, src.size() * sizeof(V)) != hipSuccess) return false;
+    return hipMemcpy(*dst, src.data(), src.size() * sizeof(V), hipMemcpyHostToDevice) == hipSuccess;
+}
+
+// ------------------------------------------------------------------ launch plumbing
+template <class T, int SRC> bool launch_q(const QParams &p, hipStream_t st) {
+    constexpr int spw = 64 / T::G;
+    const int64_t tiles = (p.nsb + spw - 1) / spw;
+    int64_t wgs = (tiles + WG_WAVES - 1) / WG_WAVES;
+    const int64_t cap = (int64_t)g_ncu * 8;
+    if (wgs > cap) wgs = cap;
+    if (wgs < 1) wgs = 1;
+    const size_t lds = (size_t)T::TAB + WG_WAVES * img_bytes<T>();
+    hipLaunchKernelGGL((k_quant<T, SRC>), dim3((unsigned)wgs), dim3(WG_THREADS), lds, st, p);
+    return hipGetLastError() == hipSuccess;
+}
+
+template <int SRC> bool launch_q8_stream(const QParams &p, hipStream_t st) {
+    constexpr int E = SRC == T_F32 ? 4 : 8, TB = (64 / (32 / E)) * 4;
+    const int64_t tiles = (p.nsb + TB - 1) / TB;
+    int64_t wgs = (tiles + WG_WAVES - 1) / WG_WAVES;
+    const int64_t cap = (int64_t)g_ncu * 16;
+    if (wgs > cap) wgs = cap;
+    if (wgs < 1) wgs = 1;
+    hipLaunchKernelGGL((k_q8_0_stream<SRC>), dim3((unsigned)wgs), dim3(WG_THREADS), 0, st, p.src, p.dst, p.nsb);
+    return hipGetLastError() == hipSuccess;
+}
+
+template <int SRC> bool dispatch_src(int type, const QParams &p, hipStream_t st) {
+    switch (type) {
+        case T_Q2_K: return launch_q<KQ2K, SRC>(p, st);
+        case T_Q3_K: return launch_q<KQ3K, SRC>(p, st);
+        case T_Q4_K: return launch_q<KQ45K<15>, SRC>(p, st);
+        case T_Q5_K: return launch_q<KQ45K<31>, SRC>(p, st);
+        case T_Q6_K: return launch_q<KQ6K, SRC>(p, st);
+        case T_Q8_0:
+            if (SRC == T_F32 || SRC == T_BF16) return launch_q8_stream<SRC == T_F32 ? T_F32 : T_BF16>(p, st);
+            return launch_q<KQ80, SRC>(p, st);
+        case T_IQ4_NL: return launch_q<KIQ4NL, SRC>(p, st);
+        case T_IQ4_XS: return launch_q<KIQ4XS, SRC>(p, st);
+        case T_IQ2_XXS: return launch_q<KIQ2XXS, SRC>(p, st);
+        case T_IQ2_XS: return launch_q<KIQ2XS, SRC>(p, st);
+        case T_IQ2_S: return launch_q<KIQ2S, SRC>(p, st);
+        case T_IQ1_S: return launch_q<KIQ1S, SRC>(p, st);
+        case T_IQ1_M: return launch_q<KIQ1M, SRC>(p, st);
+        case T_IQ3_XXS: return launch_q<KIQ3XXS, SRC>(p, st);
+        case T_IQ3_S: return launch_q<KIQ3S, SRC>(p, st);
+        default: return false;
+    }
+}
+
+// fused decode for F32 / BF16 / MXFP4 sources (the configurations' encodings); F16 and Q8_0 sources are decoded
+// to f32 by a separate pass first (exact either way)
+bool fused_src(int src) { return src == T_F32 || src == T_BF16 || src == T_MXFP4; }
+
+bool dispatch(int type, int src, const QParams &p, hipStream_t st) {
+    switch (src) {
+        case T_F32: return dispatch_src<T_F32>(type, p, st);
+        case T_BF16: return dispatch_src<T_BF16>(type, p, st);
+        case T_MXFP4: return dispatch_src<T_MXFP4>(type, p, st);
+        default: return false;
+    }
+}
+
+bool launch_decode(int src, const void *in, float *out, int64_t n, hipStream_t st) {
+    const int64_t nblk = n / 32;
+    const unsigned grid = (unsigned)((nblk + 255) / 256);
+    switch (src) {
+        case T_F32: hipLaunchKernelGGL((k_decode<T_F32>), dim3(grid), dim3(256), 0, st, (const uint8_t *)in, out, nblk); break;
+        case T_F16: hipLaunchKernelGGL((k_decode<T_F16>), dim3(grid), dim3(256), 0, st, (const uint8_t *)in, out, nblk); break;
+        case T_BF16: hipLaunchKernelGGL((k_decode<T_BF16>), dim3(grid), dim3(256), 0, st, (const uint8_t *)in, out, nblk); break;
+        case T_Q8_0: hipLaunchKernelGGL((k_decode<T_Q8_0>), dim3(grid), dim3(256), 0, st, (const uint8_t *)in, out, nblk); break;
+        case T_MXFP4: hipLaunchKernelGGL((k_decode<T_MXFP4>), dim3(grid), dim3(256), 0, st, (const uint8_t *)in, out, nblk); break;
+        default: return false;
+    }
+    return hipGetLastError() == hipSuccess;
+}
+
+bool takes_no_imatrix(int t) {
+    return t == T_Q2_K || t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_Q8_0 || t == T_IQ4_NL ||
+           t == T_IQ4_XS;
+}
+int block_len(int t) { return t == T_IQ4_NL || t == T_Q8_0 ? 32 : QK; }
+bool needs_tables(int t) { return is_search_type(t) || t == T_IQ1_M; }
+
+int64_t src_bytes(int src, int64_t n) {
+    switch (src) {
+        case T_F32: return n * 4;
+        case T_F16: case T_BF16: return n * 2;
+        case T_Q8_0: return n / 32 * 34;
+        case T_MXFP4: return n / 32 * 17;
+        default: return 0;
+    }
+}
+
+QParams params_for(int type, const void *src, void *dst, int64_t nunits, const float *qw, int64_t qw_mat,
+                   int64_t qw_mod, int64_t qw_div) {
+    QParams p{};
+    p.src = (const uint8_t *)src;
+    p.dst = (uint8_t *)dst;
+    p.nsb = nunits;
+    p.qw = type == T_Q8_0 ? nullptr : qw;   // (ggml_quantize_chunk ignores the imatrix for Q8_0)
+    p.qw_mat = qw_mat;
+    p.qw_mod = qw_mod;
+    p.qw_div = qw_div;
+    const Tabs &t = tab_of(type);
+    p.grid = t.grid;
+    p.map = t.map;
+    p.neigh = t.neigh;
+    p.map3 = t.map3;
+    p.grid_size = t.grid_size;
+    p.map_size = t.map_size;
+    p.neigh_len = t.neigh_len;
+    p.err = g_err;
+    return p;
+}
+
+bool type_ok(int type, int64_t n_per_row, bool with_imatrix) {
+    if (g_device < 0 || !gpuq_block_bytes(type)) return false;
+    if (needs_tables(type) && !tab_of(type).ok) return false;
+    if (!with_imatrix && !takes_no_imatrix(type)) return false;
+    return n_per_row > 0 && n_per_row % block_len(type) == 0;
+}
+
+// the host API's body: raw bytes of nmat x nrow x n_per_row values (src encoding) -> dst (host), synchronous
+size_t quantize_host(int src, const void *raw, int type, void *dst, int64_t nmat, int64_t nrow, int64_t n_per_row,
+                     const float *imatrix) {
+    if (nmat <= 0 || nrow <= 0 || !type_ok(type, n_per_row, imatrix != nullptr)) return 0;
+    const int64_t n = nmat * nrow * n_per_row;
+    const int64_t rb = src_bytes(src, n);
+    if (!rb || n % 32) return 0;
+    std::lock_guard<std::mutex> lock(g_mu);
+    const int bs = block_len(type);
+    const int64_t nb_row = n_per_row / bs, nb_mat = nrow * nb_row, nunits = nmat * nb_mat;
+    const size_t out_bytes = (size_t)nunits * gpuq_block_bytes(type);
+    if (!g_raw.grow((size_t)rb + 16) || !g_out.grow(out_bytes + 16)) return 0;
+    if (hipMemcpy(g_raw.p, raw, (size_t)rb, hipMemcpyHostToDevice) != hipSuccess) return 0;
+    const float *qw = nullptr;
+    if (imatrix && type != T_Q8_0) {
+        if (!g_qw.grow((size_t)nmat * n_per_row * 4)) return 0;
+        if (hipMemcpy(g_qw.p, imatrix, (size_t)nmat * n_per_row * 4, hipMemcpyHostToDevice) != hipSuccess) return 0;
+        qw = (const float *)g_qw.p;
+    }
+    const void *qsrc = g_raw.p;
+    int qsrc_type = src;
+    if (!fused_src(src)) {
+        if (!g_f32.grow((size_t)n * 4) || !launch_decode(src, g_raw.p, (float *)g_f32.p, n, 0)) return 0;
+        qsrc = g_f32.p;
+        qsrc_type = T_F32;
+    }
+    if (hipMemsetAsync(g_err, 0, sizeof(int), 0) != hipSuccess) return 0;
+    const QParams p = params_for(type, qsrc, g_out.p, nunits, qw, nb_mat, nb_row, 1);
+    if (!dispatch(type, qsrc_type, p, 0)) return 0;
+    if (hipDeviceSynchronize() != hipSuccess) return 0;
+    int err = 0;
+    if (hipMemcpy(&err, g_err, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess || err) return 0;
+    if (hipMemcpy(dst, g_out.p, out_bytes, hipMemcpyDeviceToHost) != hipSuccess) return 0;
+    return out_bytes;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ the C ABI
+extern "C" int gpuq_init(const char *tables, int device) {
+    std::lock_guard<std::mutex> lock(g_mu);
+    if (hipSetDevice(device) != hipSuccess) return 1;
+    int ncu = 0;
+    if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && ncu > 0) g_ncu = ncu;
+    if (!g_err && hipMalloc((void **)&g_err, sizeof(int)) != hipSuccess) return 4;
+    FILE *f = fopen(tables, "rb");
+    if (!f) return 2;
+    struct Rec { int type; std::vector<uint64_t> grid; std::vector<int32_t> map; std::vector<uint16_t> neigh; };
+    std::vector<Rec> recs;
+    int32_t hdr[4];
+    while (fread(hdr, sizeof hdr, 1, f) == 1) {
+        if (hdr[1] < 0 || hdr[2] < 0 || hdr[3] < 0 || hdr[1] > (1 << 20) || hdr[2] > (1 << 20) || hdr[3] > (1 << 26)) {
+            fclose(f);
+            return 3;
+        }
+        Rec r{hdr[0], std::vector<uint64_t>(hdr[1]), std::vector<int32_t>(hdr[2]), std::vector<uint16_t>(hdr[3])};
+        if (fread(r.grid.data(), 8, hdr[1], f) != (size_t)hdr[1] || fread(r.map.data(), 4, hdr[2], f) != (size_t)hdr[2] ||
+            fread(r.neigh.data(), 2, hdr[3], f) != (size_t)hdr[3]) {
+            fclose(f);
+            return 3;
+        }
+        recs.push_back(std::move(r));
+    }
+    fclose(f);
+    // validate everything before touching the device tables
+    for (const Rec &r : recs) {
+        if (r.type >= 1000) {
+            const int t = r.type - 1000;
+            if (t < 0 || t >= 64 || !is_search_type(t) || (int)r.grid.size() != expected_grid(t)) return 6;
+        } else if (r.type >= 0 && r.type < 64 && is_search_type(r.type)) {
+            if (!valid_search(r.type, r.grid, r.map, r.neigh)) return 6;
+        }
+    }
+    for (const Rec &r : recs) {
+        if (r.type >= 1000) {
+            Tabs &t = g_tabs[r.type - 1000];
+            if (!upload(&t.dq, r.grid)) return 4;
+            t.dq_size = (int)r.grid.size();
+        } else if (r.type >= 0 && r.type < 64 && is_search_type(r.type)) {
+            Tabs &t = g_tabs[r.type];
+            if (!upload(&t.grid, r.grid) || !upload(&t.map, r.map) || !upload(&t.neigh, r.neigh)) return 4;
+            t.grid_size = (int)r.grid.size();
+            t.map_size = (int)r.map.size();
+            t.neigh_len = (int)r.neigh.size();
+            if (eight_values(r.type)) {
+                std::vector<int32_t> m3(6561);
+                for (int k = 0; k < 6561; ++k) {
+                    int u = 0, rr = k;
+                    for (int i = 0; i < 8; ++i) { u |= (rr % 3) << (2 * i); rr /= 3; }
+                    m3[k] = r.map[u];
+                }
+                if (!upload(&t.map3, m3)) return 4;
+            }
+            t.ok = true;
+        }
+    }
+    g_device = device;
+    return 0;
+}
+
+extern "C" size_t gpuq_block_bytes(int type) {
+    switch (type) {
+        case T_IQ2_XXS: return 66;
+        case T_IQ2_S: return 82;
+        case T_IQ1_S: return 50;
+        case T_IQ1_M: return 56;
+        case T_IQ2_XS: return 74;
+        case T_IQ3_XXS: return 98;
+        case T_IQ3_S: return 110;
+        case T_IQ4_NL: return 18;
+        case T_IQ4_XS: return 136;
+        case T_Q2_K: return 84;
+        case T_Q3_K: return 110;
+        case T_Q4_K: return 144;
+        case T_Q5_K: return 176;
+        case T_Q6_K: return 210;
+        case T_Q8_0: return 34;
+        default: return 0;
+    }
+}
+
+extern "C" int gpuq_can_quantize(int type, int with_imatrix) {
+    return type_ok(type, block_len(type), with_imatrix != 0) ? 1 : 0;
+}
+
+extern "C" size_t gpuq_quantize_batch(int type, const float *src, void *dst, int64_t nmat, int64_t nrow,
+                                      int64_t n_per_row, const float *imatrix) {
+    return quantize_host(T_F32, src, type, dst, nmat, nrow, n_per_row, imatrix);
+}
+
+extern "C" size_t gpuq_quantize(int type, const float *src, void *dst, int64_t nrow, int64_t n_per_row,
+                                const float *imatrix) {
+    return quantize_host(T_F32, src, type, dst, 1, nrow, n_per_row, imatrix);
+}
+
+extern "C" int gpuq_can_dequantize(int src) { return src_bytes(src, 32) > 0 ? 1 : 0; }
+
+extern "C" size_t gpuq_requantize_batch(int src, const void *raw, int type, void *dst, int64_t nmat, int64_t nrow,
+                                        int64_t n_per_row, const float *imatrix) {
+    return quantize_host(src, raw, type, dst, nmat, nrow, n_per_row, imatrix);
+}
+
+extern "C" size_t gpuq_requantize(int src, const void *raw, int type, void *dst, int64_t nrow, int64_t n_per_row,
+                                  const float *imatrix) {
+    return quantize_host(src, raw, type, dst, 1, nrow, n_per_row, imatrix);
+}
+
+extern "C" size_t gpuq_quantize_dev(int type, const float *d_x, void *d_dst, int64_t nblocks, const float *d_qw,
+                                    int64_t qw_mod, int64_t qw_div, void *stream) {
+    if (block_len(type) != QK || !type_ok(type, QK, d_qw != nullptr) || nblocks <= 0 || qw_mod <= 0 || qw_div <= 0)
+        return 0;
+    if (((uintptr_t)d_x & 15) || (d_qw && ((uintptr_t)d_qw & 15)) || ((uintptr_t)d_dst & 1)) return 0;
+    const QParams p = params_for(type, d_x, d_dst, nblocks, d_qw, INT64_MAX, qw_mod, qw_div);
+    if (!dispatch(type, T_F32, p, (hipStream_t)stream)) return 0;
+    return (size_t)nblocks * gpuq_block_bytes(type);
+}
+
+extern "C" int gpuq_can_dequantize_type(int type) {
+    switch (type) {
+        case T_IQ2_XXS: case T_IQ2_XS: case T_IQ2_S: case T_IQ3_XXS: case T_IQ3_S: case T_IQ1_S: case T_IQ1_M:
+            return g_device >= 0 && tab_of(type).dq != nullptr;
+        case T_IQ4_XS: return g_device >= 0 ? 1 : 0;
+        default: return 0;
+    }
+}
+
+extern "C" size_t gpuq_dequantize_dev(int type, const void *d_q, float *d_out, int64_t nblocks, void *stream) {
+    if (!gpuq_can_dequantize_type(type) || nblocks <= 0 || ((uintptr_t)d_q & 1) || ((uintptr_t)d_out & 15)) return 0;
+    const hipStream_t st = (hipStream_t)stream;
+    const unsigned grid = (unsigned)((nblocks * 8 + 255) / 256);
+    const uint64_t *dq = tab_of(type).dq;
+    const uint8_t *q = (const uint8_t *)d_q;
+#define KDQ(T, BB) hipLaunchKernelGGL((k_dequant<T, BB>), dim3(grid), dim3(256), 0, st, q, d_out, nblocks, dq)
+    switch (type) {
+        case T_IQ2_XXS: KDQ(T_IQ2_XXS, 66); break;
+        case T_IQ2_XS: KDQ(T_IQ2_XS, 74); break;
+        case T_IQ2_S: KDQ(T_IQ2_S, 82); break;
+        case T_IQ3_XXS: KDQ(T_IQ3_XXS, 98); break;
+        case T_IQ3_S: KDQ(T_IQ3_S, 110); break;
+        case T_IQ1_S: KDQ(T_IQ1_S, 50); break;
+        case T_IQ1_M: KDQ(T_IQ1_M, 56); break;
+        case T_IQ4_XS: KDQ(T_IQ4_XS, 136); break;
+        default: return 0;
+    }
+#undef KDQ
+    return hipGetLastError() == hipSuccess ? (size_t)nblocks * QK * 4 : 0;
+}
+
+extern "C" size_t gpuq_dequantize_src_dev(int src, const void *d_raw, float *d_out, int64_t n, void *stream) {
+    if (!src_bytes(src, 32) || n <= 0 || n % 32 || ((uintptr_t)d_out & 15)) return 0;
+    if ((src == T_F32 || src == T_F16 || src == T_BF16) && ((uintptr_t)d_raw & 15)) return 0;
+    if (src == T_Q8_0 && ((uintptr_t)d_raw & 1)) return 0;
+    if (!launch_decode(src, d_raw, d_out, n, (hipStream_t)stream)) return 0;
+    return (size_t)n * 4;
+}
+
+// Device-pointer requantize (no counterpart in the reference): nmat matrices of nrow x n_per_row values stored as
+// src (F32 / BF16 / MXFP4 decoded in registers inside the quantize kernel) -> d_dst, matrix m weighted by
+// d_imatrix + m * n_per_row (or no imatrix). Asynchronous on `stream`. Returns the bytes the launch will write.
+extern "C" size_t gpuq_requantize_dev(int src, const void *d_raw, int type, void *d_dst, int64_t nmat, int64_t nrow,
+                                      int64_t n_per_row, const float *d_imatrix, void *stream) {
+    if (nmat <= 0 || nrow <= 0 || !fused_src(src) || !type_ok(type, n_per_row, d_imatrix != nullptr)) return 0;
+    if (((uintptr_t)d_raw & 15) || (d_imatrix && ((uintptr_t)d_imatrix & 15)) || ((uintptr_t)d_dst & 1)) return 0;
+    if ((n_per_row * (src == T_F32 ? 4 : 2)) % 16 && src != T_MXFP4) return 0;
+    const int bs = block_len(type);
+    const int64_t nb_row = n_per_row / bs, nb_mat = nrow * nb_row, nunits = nmat * nb_mat;
+    const QParams p = params_for(type, d_raw, d_dst, nunits, d_imatrix, nb_mat, nb_row, 1);
+    if (!dispatch(type, src, p, (hipStream_t)stream)) return 0;
+    return (size_t)nunits * gpuq_block_bytes(type);
+}
+
+// Reads and clears the search-failure flag (no counterpart in the reference, whose kernels trap instead): 1 when a
+// device-API launch since the last call found a key with no candidate point (non-finite input or a bad table).
+extern "C" int gpuq_take_error(void) {
+    if (!g_err) return 0;
+    int err = 0;
+    if (hipDeviceSynchronize() != hipSuccess) return 1;
+    if (hipMemcpy(&err, g_err, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess) return 1;
+    (void)hipMemset(g_err, 0, sizeof(int));
+    return err;
+}

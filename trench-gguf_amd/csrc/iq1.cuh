@@ -1,0 +1,385 @@
+// trench-gguf_amd/csrc/iq1.cuh - IQ1_S and IQ1_M on gfx950.
+//
+// Semantics: ggml's quantize_row_iq1_s_impl / quantize_row_iq1_m_impl as the reference restates them
+// (gpuq/gpuq.hip:199-232, 389-688). Per lane: one 32-weight (IQ1_S) or 16-weight (IQ1_M) block.
+//  - The stable sort by value is computed as ranks, rank_i = #{j < i: x_j <= x_i} + #{j > i: x_j < x_i}, which is
+//    the position of element i in glibc's stable order; the prefix sums then run in that order, serially, as ggml's.
+//  - The (i1, i2) partition search runs every candidate in ggml's order on the lane, so its cross-multiplied
+//    acceptance chain is ggml's exactly. Its loop indices are wave-uniform, so the prefix arrays are indexed through
+//    uniform (M0-relative) register addressing.
+//  - IQ1_M's final least-squares d over all 256 weights is a lane-to-lane chain in ggml's index order.
+// Tables: the 2048-point IQ1 grid and its base-3 key map in LDS (the IQ1 levels are always 0..2), lists in HBM.
+#pragma once
+#include "iq2.cuh"
+
+#define EPS_IQ1S 1e-12f
+#define EPS_IQ1M 1e-7f
+#define IQ1_DELTA 0.125f
+
+// x_p = {-1+d, d, 1+d}, x_m = {-1-d, -d, 1-d}: the value of level l (0..2) for shift +1 / -1
+DEV float iq1_val(int l, bool minus) {
+    const float a = minus ? -1 - IQ1_DELTA : -1 + IQ1_DELTA;
+    const float b = minus ? -IQ1_DELTA : IQ1_DELTA;
+    const float c = minus ? 1 - IQ1_DELTA : 1 + IQ1_DELTA;
+    return l == 0 ? a : (l == 1 ? b : c);
+}
+
+// iq1_find_best_neighbour2 over a list (gpuq/gpuq.hip:199-232); -1 when no neighbour has a finite distance (the
+// reference then scans the whole grid with an out-of-block read; that case is reported as an error here)
+DEV int nb_best_iq1(const uint16_t *nb, const uint64_t *grid, const float *xv, const float *w, float scale,
+                    bool minus) {
+    const int cnt = nb[0];
+    float best = FLT_MAX;
+    int gi = -1;
+    for (int j = 1; j <= cnt; ++j) {
+        const int idx = nb[j];
+        const uint64_t pt = grid[idx];
+        const uint32_t lo = (uint32_t)pt, hi = (uint32_t)(pt >> 32);
+        float d2 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int b = (int)(((i < 4 ? lo : hi) >> (8 * (i % 4))) & 0xffu);
+            const float q = iq1_val((b - 1) / 2, minus);
+            const float diff = scale * q - xv[i];
+            d2 += w[i] * diff * diff;
+        }
+        if (d2 < best) { best = d2; gi = idx; }
+    }
+    return gi;
+}
+
+// position of element i in the stable ascending order of x
+template <int N> DEV void stable_ranks(const float (&x)[N], Lv<N> &R) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        int r = 0;
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            if (j < i) r += x[j] <= x[i];
+            else if (j > i) r += x[j] < x[i];
+        }
+        R.put(i, (uint32_t)r);
+    }
+}
+
+// 2-sum chain over the group in lane (index) order
+template <int G, int N> DEV void grp_chain_sum2(const float (&a)[N], const float (&b)[N], int g, float &sa, float &sb) {
+    float acc_a = 0.f, acc_b = 0.f;
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+        float ta = acc_a, tb = acc_b;
+        if (g == j) {
+#pragma unroll
+            for (int i = 0; i < N; ++i) { ta += a[i]; tb += b[i]; }
+        }
+        acc_a = grp_bcast<G>(ta, j);
+        acc_b = grp_bcast<G>(tb, j);
+    }
+    sa = acc_a;
+    sb = acc_b;
+}
+
+// ------------------------------------------------------------------ IQ1_S (gpuq/gpuq.hip:389-514)
+// block: d qs[32] qh[8] u16 (50 bytes); lane g = 32-weight block g
+struct KIQ1S : Iq8Tab<2048> {
+    static constexpr int BS = QK, G = 8, N = 32, BB = 50;
+    static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
+                          const QParams &p) {
+        const uint64_t *grid = Iq8Tab<2048>::grid(lds);
+        const int32_t *map3 = Iq8Tab<2048>::map3(lds);
+        const float xp0 = -1 + IQ1_DELTA, xp1 = IQ1_DELTA, xp2 = 1 + IQ1_DELTA;
+        const float xm0 = -1 - IQ1_DELTA, xm1 = -IQ1_DELTA, xm2 = 1 - IQ1_DELTA;
+        float qv[N], sq[N], weight[N];
+        load_qw<N>(qwp, qv);
+#pragma unroll
+        for (int i = 0; i < N; ++i) sq[i] = x[i] * x[i];
+        const float sigma2 = 2 * grp_chain_sum<G, N>(sq, g) / QK;
+#pragma unroll
+        for (int i = 0; i < N; ++i) weight[i] = qv[i] * sqrtf(sigma2 + sq[i]);
+        float mx = fabsf(x[0]);
+#pragma unroll
+        for (int i = 1; i < N; ++i) mx = fmax_sel(mx, fabsf(x[i]));
+        bool live = false, minus = false;
+        float scale = 0.f;
+        int gi4[4] = {0, 0, 0, 0};
+        if (!(mx < EPS_IQ1S)) {
+            Lv<N> R;
+            stable_ranks<N>(x, R);
+            float sumx[N + 1], sumw[N + 1];
+            sumx[0] = sumw[0] = 0;
+#pragma unroll
+            for (int j = 0; j < N; ++j) {
+                float tx = 0.f, tw = 0.f;
+#pragma unroll
+                for (int i = 0; i < N; ++i)
+                    if (R.get(i) == (uint32_t)j) { tx = weight[i] * x[i]; tw = weight[i]; }
+                sumx[j + 1] = sumx[j] + tx;
+                sumw[j + 1] = sumw[j] + tw;
+            }
+            float best_score = -FLT_MAX;
+            scale = mx;
+            int besti1 = -1, besti2 = -1, best_shift = 0;
+            for (int i1 = 0; i1 <= N; ++i1) {
+                const float a_x = sumx[i1] - sumx[0], a_w = sumw[i1] - sumw[0];
+                const float s1x = sumx[i1], s1w = sumw[i1];
+                for (int i2 = i1; i2 <= N; ++i2) {
+                    const float s2x = sumx[i2], s2w = sumw[i2];
+                    float sumqx = a_x * xp0 + (s2x - s1x) * xp1 + (sumx[N] - s2x) * xp2;
+                    float sumq2 = a_w * xp0 * xp0 + (s2w - s1w) * xp1 * xp1 + (sumw[N] - s2w) * xp2 * xp2;
+                    if (sumq2 > 0 && sumqx * sumqx > best_score * sumq2) {
+                        scale = sumqx / sumq2;
+                        best_score = scale * sumqx;
+                        besti1 = i1; besti2 = i2; best_shift = 1;
+                    }
+                    sumqx = a_x * xm0 + (s2x - s1x) * xm1 + (sumx[N] - s2x) * xm2;
+                    sumq2 = a_w * xm0 * xm0 + (s2w - s1w) * xm1 * xm1 + (sumw[N] - s2w) * xm2 * xm2;
+                    if (sumq2 > 0 && sumqx * sumqx > best_score * sumq2) {
+                        scale = sumqx / sumq2;
+                        best_score = scale * sumqx;
+                        besti1 = i1; besti2 = i2; best_shift = -1;
+                    }
+                }
+            }
+            if (besti1 < 0 || besti2 < 0 || best_shift == 0) {
+                scale = 0.f;
+            } else {
+                live = true;
+                const bool flip = scale < 0;
+                if (flip) { scale = -scale; best_shift = -best_shift; }
+                minus = best_shift != 1;
+                bool all_on_grid = true;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    int k3 = 0, p3 = 1;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int r = (int)R.get(8 * k + j);
+                        int l = r < besti1 ? 0 : (r < besti2 ? 1 : 2);
+                        if (flip) l = 2 - l;
+                        k3 += l * p3;
+                        p3 *= 3;
+                    }
+                    const int m = map3[k3];
+                    int gi = m;
+                    if (m < 0) {
+                        all_on_grid = false;
+                        gi = nb_best_iq1(p.neigh + (-m - 1), grid, x + 8 * k, weight + 8 * k, scale, minus);
+                        if (gi < 0) { flag_err(p); gi = 0; }
+                    }
+                    gi4[k] = gi;
+                }
+                if (!all_on_grid) {
+                    float sumqx = 0, sumq2 = 0;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const uint64_t pt = grid[gi4[k]];
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) {
+                            const int b = (int)((pt >> (8 * j)) & 0xffu);
+                            const float w = weight[8 * k + j];
+                            const float q = iq1_val((b - 1) / 2, minus);
+                            sumqx += w * q * x[8 * k + j];
+                            sumq2 += w * q * q;
+                        }
+                    }
+                    if (sumqx > 0 && sumq2 > 0) scale = sumqx / sumq2;
+                }
+            }
+        }
+        uint32_t h = 0;
+        if (live) {
+            img_or32(img, boff + 2 + 4 * g, (uint32_t)(gi4[0] & 255) | ((uint32_t)(gi4[1] & 255) << 8) |
+                                               ((uint32_t)(gi4[2] & 255) << 16) | ((uint32_t)(gi4[3] & 255) << 24));
+#pragma unroll
+            for (int k = 0; k < 4; ++k) h |= (uint32_t)(gi4[k] >> 8) << (3 * k);
+        }
+        const float max_scale = grp_max<G>(scale);
+        if (max_scale) {
+            const float d = max_scale / 15;
+            if (g == 0) img_or16(img, boff, f2h(d * 1.125f));
+            const float id = 1 / d;
+            int l = imax(0, imin(7, nint(0.5f * (id * scale - 1))));
+            if (live && minus) l |= 8;
+            h |= (uint32_t)l << 12;
+        }
+        img_or16(img, boff + 34 + 2 * g, h & 0xffffu);
+    }
+};
+
+// ------------------------------------------------------------------ IQ1_M (gpuq/gpuq.hip:516-688)
+// block: qs[32] qh[16] scales[8] (56 bytes); lane g = 16-weight block g
+struct KIQ1M : Iq8Tab<2048> {
+    static constexpr int BS = QK, G = 16, N = 16, BB = 56;
+    static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
+                          const QParams &p) {
+        const uint64_t *grid = Iq8Tab<2048>::grid(lds);
+        const int32_t *map3 = Iq8Tab<2048>::map3(lds);
+        const float xp0 = -1 + IQ1_DELTA, xp1 = IQ1_DELTA, xp2 = 1 + IQ1_DELTA;
+        const float xm0 = -1 - IQ1_DELTA, xm1 = -IQ1_DELTA, xm2 = 1 - IQ1_DELTA;
+        float qv[N], sq[N], weight[N];
+        load_qw<N>(qwp, qv);
+#pragma unroll
+        for (int i = 0; i < N; ++i) sq[i] = x[i] * x[i];
+        const float sigma2 = 2 * grp_chain_sum<G, N>(sq, g) / QK;
+#pragma unroll
+        for (int i = 0; i < N; ++i) weight[i] = qv[i] * sqrtf(sigma2 + sq[i]);
+        float mx = fabsf(x[0]);
+#pragma unroll
+        for (int i = 1; i < N; ++i) mx = fmax_sel(mx, fabsf(x[i]));
+        bool live = false;
+        int best_k = 0;       // the shift combination (0 for a skipped block, masks[0] = 0)
+        float scale = 0.f;
+        int gi2[2] = {0, 0};
+        if (!(mx < EPS_IQ1M)) {
+            Lv<N> R;
+            stable_ranks<N>(x, R);
+            float px0[N + 1], px1[N + 1], pw0[N + 1], pw1[N + 1];
+            px0[0] = px1[0] = 0;
+            pw0[0] = pw1[0] = 0;
+#pragma unroll
+            for (int j = 0; j < N; ++j) {
+                float tx = 0.f, tw = 0.f;
+                int hsel = 0;
+#pragma unroll
+                for (int i = 0; i < N; ++i)
+                    if (R.get(i) == (uint32_t)j) { tx = weight[i] * x[i]; tw = weight[i]; hsel = i < N / 2 ? 0 : 1; }
+                px0[j + 1] = hsel == 0 ? px0[j] + tx : px0[j];
+                px1[j + 1] = hsel == 1 ? px1[j] + tx : px1[j];
+                pw0[j + 1] = hsel == 0 ? pw0[j] + tw : pw0[j];
+                pw1[j + 1] = hsel == 1 ? pw1[j] + tw : pw1[j];
+            }
+            const float txs0 = px0[N], txs1 = px1[N], tws0 = pw0[N], tws1 = pw1[N];
+            const float p2 = xp2, m2 = xm2;
+            const float cp1 = xp0 * xp0 - xp1 * xp1, cp2 = xp1 * xp1 - xp2 * xp2;
+            const float cm1 = xm0 * xm0 - xm1 * xm1, cm2 = xm1 * xm1 - xm2 * xm2;
+            float best_score = -FLT_MAX;
+            scale = mx;
+            int besti1 = -1, besti2 = -1, bk = -1;
+            for (int i1 = 0; i1 <= N; ++i1) {
+                const float a0x = px0[i1], a1x = px1[i1], a0w = pw0[i1], a1w = pw1[i1];
+                for (int i2 = i1; i2 <= N; ++i2) {
+                    float qx_p[2], qx_m[2], q2_p[2], q2_m[2];
+                    {
+                        const float sx = a0x + px0[i2];
+                        qx_p[0] = txs0 * p2 - sx;
+                        qx_m[0] = txs0 * m2 - sx;
+                        q2_p[0] = tws0 * p2 * p2 + a0w * cp1 + pw0[i2] * cp2;
+                        q2_m[0] = tws0 * m2 * m2 + a0w * cm1 + pw0[i2] * cm2;
+                    }
+                    {
+                        const float sx = a1x + px1[i2];
+                        qx_p[1] = txs1 * p2 - sx;
+                        qx_m[1] = txs1 * m2 - sx;
+                        q2_p[1] = tws1 * p2 * p2 + a1w * cp1 + pw1[i2] * cp2;
+                        q2_m[1] = tws1 * m2 * m2 + a1w * cm1 + pw1[i2] * cm2;
+                    }
+                    float sumqx[4], sumq2[4];
+                    sumqx[0] = qx_p[0] + qx_p[1];
+                    sumqx[1] = qx_p[0] + qx_m[1];
+                    sumqx[2] = qx_m[0] + qx_p[1];
+                    sumqx[3] = qx_m[0] + qx_m[1];
+                    sumq2[0] = q2_p[0] + q2_p[1];
+                    sumq2[1] = q2_p[0] + q2_m[1];
+                    sumq2[2] = q2_m[0] + q2_p[1];
+                    sumq2[3] = q2_m[0] + q2_m[1];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        if (sumq2[k] > 0 && sumqx[k] * sumqx[k] > best_score * sumq2[k]) {
+                            scale = sumqx[k] / sumq2[k];
+                            best_score = scale * sumqx[k];
+                            besti1 = i1; besti2 = i2; bk = k;
+                        }
+                    }
+                }
+            }
+            if (besti1 < 0 || besti2 < 0 || bk < 0) {
+                scale = 0.f;
+            } else {
+                live = true;
+                const bool flip = scale < 0;
+                if (flip) { scale = -scale; bk = 3 - bk; }
+                best_k = bk;
+                bool all_on_grid = true;
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const bool minus = k == 0 ? !(bk < 2) : !(bk % 2 == 0);
+                    int k3 = 0, p3 = 1;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int r = (int)R.get(8 * k + j);
+                        int l = r < besti1 ? 0 : (r < besti2 ? 1 : 2);
+                        if (flip) l = 2 - l;
+                        k3 += l * p3;
+                        p3 *= 3;
+                    }
+                    const int m = map3[k3];
+                    int gi = m;
+                    if (m < 0) {
+                        all_on_grid = false;
+                        gi = nb_best_iq1(p.neigh + (-m - 1), grid, x + 8 * k, weight + 8 * k, scale, minus);
+                        if (gi < 0) { flag_err(p); gi = 0; }
+                    }
+                    gi2[k] = gi;
+                }
+                if (!all_on_grid) {
+                    float sqx = 0, sq2 = 0;
+#pragma unroll
+                    for (int k = 0; k < 2; ++k) {
+                        const bool minus = k == 0 ? !(bk < 2) : !(bk % 2 == 0);
+                        const uint64_t pt = grid[gi2[k]];
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) {
+                            const int b = (int)((pt >> (8 * j)) & 0xffu);
+                            const float w = weight[8 * k + j];
+                            const float q = iq1_val((b - 1) / 2, minus);
+                            sqx += w * q * x[8 * k + j];
+                            sq2 += w * q * q;
+                        }
+                    }
+                    if (sqx > 0 && sq2 > 0) scale = sqx / sq2;
+                }
+            }
+        }
+        uint32_t qh = 0;
+        if (live) {
+            img_or16(img, boff + 2 * g, (uint32_t)(gi2[0] & 255) | ((uint32_t)(gi2[1] & 255) << 8));
+            qh = (uint32_t)((gi2[0] >> 8) | ((gi2[1] >> 8) << 4));
+        }
+        const float max_scale = grp_max<G>(scale);
+        if (!max_scale) {
+            img_or8(img, boff + 32 + g, qh);
+            return;
+        }
+        float d = max_scale / 15;
+        const float id = 1 / d;
+        const int l = imax(0, imin(7, nint(0.5f * (id * scale - 1))));
+        const uint32_t masks = best_k == 0 ? 0x00u : best_k == 1 ? 0x80u : best_k == 2 ? 0x08u : 0x88u;
+        qh |= masks;
+        img_or8(img, boff + 32 + g, qh);
+        // ggml's least-squares d over all 256 weights, with each block's stored point (grid[0] for a skipped one)
+        float tqx[16], tq2[16];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const bool minus = k == 0 ? !(best_k < 2) : !(best_k % 2 == 0);
+            const uint64_t pt = grid[live ? gi2[k] : 0];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int b = (int)((pt >> (8 * j)) & 0xffu);
+                const float w = weight[8 * k + j];
+                const float q = iq1_val((b - 1) / 2, minus) * (2 * l + 1);
+                tqx[8 * k + j] = w * q * x[8 * k + j];
+                tq2[8 * k + j] = w * q * q;
+            }
+        }
+        float sumqx_f, sumq2_f;
+        grp_chain_sum2<G, 16>(tqx, tq2, g, sumqx_f, sumq2_f);
+        if (sumq2_f > 0) d = sumqx_f / sumq2_f;
+        const uint32_t s = f2h(d * 1.1125f);
+        // scales: 4 u16 words, block ib's 3 bits at word ib/4, bits 3*(ib%4); the fp16 nibbles at bits 12..15
+        img_or16(img, boff + 48 + 2 * (g / 4), (uint32_t)(l << (3 * (g % 4))));
+        if (g < 4) {
+            const uint32_t nib = (s >> (4 * g)) & 0xfu;
+            img_or16(img, boff + 48 + 2 * g, nib << 12);
+        }
+    }
+};

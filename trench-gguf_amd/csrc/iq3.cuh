@@ -1,0 +1,215 @@
+// trench-gguf_amd/csrc/iq3.cuh - IQ3_XXS and IQ3_S on gfx950.
+//
+// Semantics: ggml's quantize_row_iq3_xxs_impl / quantize_row_iq3_s_impl as the reference restates them
+// (gpuq/gpuq.hip:971-1283). Per lane: one 32-weight sub-block of eight 4-value groups. The whole 4096-entry 3-bit
+// key map (every key is reachable: levels 0..7) and the grid (uint32 points, byte i = 2l+1) sit in LDS; neighbour
+// lists stay in HBM. A group's levels are kept as its point's 4 bytes, one dword a group.
+#pragma once
+#include "iq2.cuh"
+
+#define EPS_IQ3XXS 1e-8f
+#define NKEY8 4096
+
+template <int GRID> struct Iq4Tab {
+    static constexpr int GRIDB = GRID * 4;
+    static constexpr int TAB = (GRIDB + NKEY8 * 4 + 15) & ~15;
+    static DEV void stage(const QParams &p, uint8_t *lds) {
+        uint32_t *gd = (uint32_t *)lds;
+        for (int i = threadIdx.x; i < GRID; i += WG_THREADS) gd[i] = (uint32_t)p.grid[i];
+        int32_t *md = (int32_t *)(lds + GRIDB);
+        for (int i = threadIdx.x; i < NKEY8; i += WG_THREADS) md[i] = p.map[i];
+    }
+    static DEV const uint32_t *grid(const uint8_t *lds) { return (const uint32_t *)lds; }
+    static DEV const int32_t *map(const uint8_t *lds) { return (const int32_t *)(lds + GRIDB); }
+};
+
+DEV int key3_of_point(uint32_t pt) {
+    int u = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u |= (int)((((pt >> (8 * i)) & 0xffu) - 1) >> 1) << (3 * i);
+    return u;
+}
+
+// iq3_find_best_neighbour (gpuq/gpuq.hip:971-992)
+DEV int nb_best4(const uint16_t *nb, const uint32_t *grid, const float *xv, const float *wa, float scale) {
+    const int cnt = nb[0];
+    float best = FLT_MAX;
+    int gi = -1;
+    for (int j = 1; j <= cnt; ++j) {
+        const int idx = nb[j];
+        const uint32_t pt = grid[idx];
+        float d2 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float q = (float)((pt >> (8 * i)) & 0xffu);
+            const float diff = scale * q - xv[i];
+            d2 += wa[i] * diff * diff;
+        }
+        if (d2 < best) { best = d2; gi = idx; }
+    }
+    return gi;
+}
+
+DEV int group_key8(const float *xv, float id) {
+    int u = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u |= imax(0, imin(7, nint(0.5f * (id * xv[i] - 1)))) << (3 * i);
+    return u;
+}
+
+// the shared IQ3 32-weight search; returns the sub-block scale, P = its 8 group points, live = not skipped
+template <bool XXS, int GRID>
+DEV float iq3_search(const float (&x)[32], const float (&qv)[32], float sigma2, const QParams &p, const uint8_t *lds,
+                     uint32_t (&P)[8], uint32_t (&bsg)[4], bool &live) {
+    const uint32_t *grid = Iq4Tab<GRID>::grid(lds);
+    const int32_t *map = Iq4Tab<GRID>::map(lds);
+    float weight[32], waux[32], xval[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) weight[i] = qv[i] * sqrtf(sigma2 + x[i] * x[i]);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) waux[i] = sqrtf(weight[i]);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        bsg[k] = XXS ? signs_even8(x + 8 * k, weight + 8 * k, xval + 8 * k) : signs_plain8(x + 8 * k, xval + 8 * k);
+    float mx = xval[0];
+#pragma unroll
+    for (int i = 1; i < 32; ++i) mx = fmax_sel(mx, xval[i]);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) P[k] = 0x01010101u;          // L = 0
+    live = XXS ? !(mx < EPS_IQ3XXS) : (mx != 0.f);
+    if (!live) return 0.f;
+    float best = 0;
+    float scale = mx / 15;
+    bool on_grid[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) on_grid[k] = XXS;             // (IQ3_S starts from "not on the grid")
+    constexpr int NT = XXS ? 15 : 9;
+    for (int is = -NT; is <= NT; ++is) {
+        const float id = (15 + is * 0.2f) / mx;
+        const float this_scale = 1 / id;
+        uint32_t Pa[8];
+        bool og[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int m = map[group_key8(xval + 4 * k, id)];
+            og[k] = m >= 0;
+            const int gi = m >= 0 ? m : nb_best4(p.neigh + (-m - 1), grid, xval + 4 * k, waux + 4 * k, this_scale);
+            if (gi < 0) flag_err(p);
+            Pa[k] = grid[gi < 0 ? 0 : gi];
+        }
+        float sumqx, sumq2;
+        sums_q<32>(weight, xval, Pa, sumqx, sumq2);
+        if (sumq2 > 0 && sumqx * sumqx > best * sumq2) {
+            scale = sumqx / sumq2;
+            best = scale * sumqx;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) { P[k] = Pa[k]; on_grid[k] = og[k]; }
+        }
+    }
+    bool any_off = false;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) any_off |= !on_grid[k];
+    if (any_off && scale > 0) {
+        const float id = 1 / scale;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            if (XXS && on_grid[k]) continue;                  // (IQ3_S re-searches every group)
+            const int m = map[group_key8(xval + 4 * k, id)];
+            const int gi = m >= 0 ? m : nb_best4(p.neigh + (-m - 1), grid, xval + 4 * k, waux + 4 * k, scale);
+            if (gi < 0) flag_err(p);
+            P[k] = grid[gi < 0 ? 0 : gi];
+        }
+        float sumqx, sumq2;
+        sums_q<32>(weight, xval, P, sumqx, sumq2);
+        if (sumq2 > 0) scale = sumqx / sumq2;
+    }
+    if (scale < 0) {
+        scale = -scale;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) bsg[k] = XXS ? ((~bsg[k]) & 127) : ((~bsg[k]) & 255);
+    }
+    return scale;
+}
+
+// IQ3_XXS: block d qs[96] = 64 grid bytes, then 8 u32 signs-and-scales (98 bytes)
+struct KIQ3XXS : Iq4Tab<256> {
+    static constexpr int BS = QK, G = 8, N = 32, BB = 98;
+    static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
+                          const QParams &p) {
+        const int32_t *map = Iq4Tab<256>::map(lds);
+        float qv[N], sq[N];
+        load_qw<N>(qwp, qv);
+#pragma unroll
+        for (int i = 0; i < N; ++i) sq[i] = x[i] * x[i];
+        const float sigma2 = 2 * grp_chain_sum<G, N>(sq, g) / QK;
+        uint32_t P[8], bsg[4];
+        bool live;
+        const float scale = iq3_search<true, 256>(x, qv, sigma2, p, lds, P, bsg, live);
+        const float max_scale = grp_max<G>(live ? scale : 0.f);
+        if (!max_scale) return;                               // qs all zero, d = 0
+        uint32_t q3lo = 0, q3hi = 0, sas = 0;
+        if (live) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int gi = map[key3_of_point(P[k])];
+                if (gi < 0) flag_err(p);
+                if (k < 4) q3lo |= (uint32_t)(gi & 255) << (8 * k);
+                else q3hi |= (uint32_t)(gi & 255) << (8 * (k - 4));
+            }
+            sas = bsg[0] | (bsg[1] << 7) | (bsg[2] << 14) | (bsg[3] << 21);
+        }
+        const float d = max_scale / 31;
+        if (g == 0) img_or16(img, boff, f2h(d * 1.0125f));
+        const float id = 1 / d;
+        const int l = imax(0, imin(15, nint(0.5f * (id * (live ? scale : 0.f) - 1))));
+        sas |= (uint32_t)l << 28;
+        img_or32(img, boff + 2 + 8 * g, q3lo);
+        img_or32(img, boff + 6 + 8 * g, q3hi);
+        img_or32(img, boff + 2 + 64 + 4 * g, sas);
+    }
+};
+
+// IQ3_S: block d qs[64] qh[8] signs[32] scales[4] (110 bytes). A skipped (all-zero) sub-block does not advance the
+// qs / signs cursors (ggml's quirk, kept by the reference): the next live sub-block takes its slot.
+struct KIQ3S : Iq4Tab<512> {
+    static constexpr int BS = QK, G = 8, N = 32, BB = 110;
+    static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
+                          const QParams &p) {
+        const int32_t *map = Iq4Tab<512>::map(lds);
+        float qv[N], sq[N];
+        load_qw<N>(qwp, qv);
+#pragma unroll
+        for (int i = 0; i < N; ++i) sq[i] = x[i] * x[i];
+        const float sigma2 = 2 * grp_chain_sum<G, N>(sq, g) / QK;
+        uint32_t P[8], bsg[4];
+        bool live;
+        const float scale = iq3_search<false, 512>(x, qv, sigma2, p, lds, P, bsg, live);
+        // the slot of this sub-block: the number of live sub-blocks before it
+        const uint64_t bal = __ballot(live);
+        const int gbase = lane_id() & ~(G - 1);
+        const uint32_t gm = (uint32_t)(bal >> gbase) & ((1u << G) - 1);
+        const int pos = __popc(gm & ((1u << g) - 1));
+        if (live) {
+            uint32_t qlo = 0, qhi = 0, qh = 0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int gi = map[key3_of_point(P[k])];
+                if (gi < 0) flag_err(p);
+                if (k < 4) qlo |= (uint32_t)(gi & 255) << (8 * k);
+                else qhi |= (uint32_t)(gi & 255) << (8 * (k - 4));
+                qh |= (uint32_t)((gi >> 8) & 1) << k;
+            }
+            img_or32(img, boff + 2 + 8 * pos, qlo);
+            img_or32(img, boff + 6 + 8 * pos, qhi);
+            img_or8(img, boff + 66 + g, qh);
+            img_or32(img, boff + 74 + 4 * pos, bsg[0] | (bsg[1] << 8) | (bsg[2] << 16) | (bsg[3] << 24));
+        }
+        const float max_scale = grp_max<G>(live ? scale : 0.f);
+        if (!max_scale) return;
+        const float d = max_scale / 31;
+        if (g == 0) img_or16(img, boff, f2h(d * 1.033f));
+        const float id = 1 / d;
+        const int l = imax(0, imin(15, nint(0.5f * (id * (live ? scale : 0.f) - 1))));
+        img_or8(img, boff + 106 + g / 2, (uint32_t)(l << (4 * (g % 2))));
+    }
+};
