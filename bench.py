@@ -1,0 +1,279 @@
+#!/usr/bin/env python3
+"""bench.py - throughput of the MI355X GGUF quantizer on the configured synthetic workloads.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
+
+One "step" is one pass of the quantizer over one workload tensor already resident in HBM (the device entry point
+gpuq_requantize_dev: source bytes decoded in registers, quantized, blocks written to HBM). The headline line is the
+Q4_K-with-imatrix workload on a 2048 x 7168 BF16 tensor (N(0, 0.02) plus 0.1% outliers at +-8 sigma, a log-normal
+imatrix); `per_type` adds Q6_K on the same tensor, Q8_0 on a 4096 x 4096 F32 tensor, IQ2_XXS on 256 x 2048 x 7168
+BF16 experts and IQ1_S / IQ1_M on 384 x 2048 x 7168 MXFP4 experts. Kernel time comes from HIP events on the launch
+stream; inputs that fit the 256 MB Infinity Cache are rotated over enough copies that every launch reads HBM.
+
+Each entry carries a roofline (HBM bytes for Q8_0, VALU operations for the searches: the sequential algorithm's
+fp32/int operation count per weight, measured by the op-counting build of the CPU oracle on a sample of the same
+tensor) and the CPU baseline: the oracle (a C restatement of ggml_quantize_chunk, -O2 without FMA) on all the host
+cores this process may use, timed on a bounded sample of the same tensor, whose bytes are also compared with the
+GPU's as a spot check.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "trench-gguf_amd"))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+
+METRIC = "Mweights/s per type (Q8_0, Q4_K, IQ2_XXS, IQ1_M) on 1 MI355X; % VALU/HBM peak"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+VALU_PEAK_TOPS = 39.3          # 256 CUs x 64 lanes x 2.4 GHz, non-packed fp32/int lane-operations, T/s
+MALL_BYTES = 256 << 20         # Infinity Cache
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_threads():
+    try:
+        return max(1, min(len(os.sched_getaffinity(0)), 64))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+class Workload:
+    """a synthetic tensor in HBM (source bytes, imatrix) plus its host-side sample for the CPU leg"""
+
+    def __init__(self, name, src, nmat, nrow, ncol, raw, imatrix):
+        self.name, self.src, self.nmat, self.nrow, self.ncol = name, src, nmat, nrow, ncol
+        self.raw, self.imatrix = raw, imatrix
+        self.n = nmat * nrow * ncol
+
+
+def make_f32(torch, gen, shape, sigma):
+    return (torch.randn(shape, device="cuda", generator=gen) * sigma).contiguous()
+
+
+def wl_c1(torch, gpuq):
+    g = torch.Generator(device="cuda").manual_seed(0)
+    x = make_f32(torch, g, (4096, 4096), 0.02)
+    return Workload("F32 4096x4096 N(0,0.02), seed 0", gpuq.F32, 1, 4096, 4096, x, None)
+
+
+def wl_c2(torch, gpuq):
+    g = torch.Generator(device="cuda").manual_seed(1)
+    x = make_f32(torch, g, (2048, 7168), 0.02).reshape(-1)
+    nout = x.numel() // 1000                                     # 0.1% outliers at +-8 sigma
+    pos = torch.randperm(x.numel(), device="cuda", generator=g)[:nout]
+    sgn = torch.randint(0, 2, (nout,), device="cuda", generator=g).float() * 2 - 1
+    x[pos] = sgn * 0.16
+    raw = x.to(torch.bfloat16).contiguous()                       # RNE to BF16
+    im = torch.exp(torch.randn(1, 7168, device="cuda", generator=g) * 1.5).contiguous()
+    return Workload("BF16 2048x7168 N(0,0.02) + 0.1% outliers at +-8 sigma, log-normal(0,1.5) imatrix",
+                    gpuq.BF16, 1, 2048, 7168, raw, im)
+
+
+def wl_c3(torch, gpuq, nexp=256):
+    g = torch.Generator(device="cuda").manual_seed(2)
+    sig = torch.rand(nexp, 1, 1, device="cuda", generator=g) * 0.02 + 0.01
+    raw = torch.empty((nexp, 2048, 7168), dtype=torch.bfloat16, device="cuda")
+    for e in range(0, nexp, 16):                                  # (bounded temporaries)
+        raw[e:e + 16] = (torch.randn((min(16, nexp - e), 2048, 7168), device="cuda", generator=g)
+                         * sig[e:e + 16]).to(torch.bfloat16)
+    im = torch.exp(torch.randn(nexp, 7168, device="cuda", generator=g) * 1.5).contiguous()
+    return Workload("BF16 %dx2048x7168 experts, N(0, s_e), s_e ~ U[0.01,0.03], per-expert log-normal(0,1.5) imatrix"
+                    % nexp, gpuq.BF16, nexp, 2048, 7168, raw.reshape(-1), im)
+
+
+def wl_c4(torch, gpuq, nexp=384):
+    g = torch.Generator(device="cuda").manual_seed(3)
+    nblk = nexp * 2048 * 7168 // 32
+    raw = torch.randint(0, 256, (nblk, 17), dtype=torch.uint8, device="cuda", generator=g)
+    raw[:, 0] = (127 + torch.randint(-8, -3, (nblk,), device="cuda", generator=g)).to(torch.uint8)
+    im = torch.exp(torch.randn(nexp, 7168, device="cuda", generator=g) * 1.5).contiguous()
+    return Workload("MXFP4 %dx2048x7168 experts, e8m0 exponents U{-8..-4}, uniform e2m1 codes, per-expert "
+                    "log-normal(0,1.5) imatrix" % nexp, gpuq.MXFP4, nexp, 2048, 7168, raw.reshape(-1), im)
+
+
+def time_gpu(torch, gq, gpuq, wl, typ, steps, warmup):
+    """average kernel time (ms) of gpuq_requantize_dev over `steps` launches, HIP events on the launch stream"""
+    bpw = {gpuq.F32: 4.0, gpuq.BF16: 2.0, gpuq.MXFP4: 17 / 32}[wl.src]
+    in_bytes = wl.n * bpw
+    copies = 1
+    if in_bytes < 2 * MALL_BYTES:                                 # rotate copies so each launch reads HBM
+        copies = int(2 * MALL_BYTES // in_bytes) + 1
+    raws = [wl.raw] + [wl.raw.clone() for _ in range(copies - 1)]
+    out_bytes = wl.n // gpuq.BLOCK[typ] * gq.gpuq_block_bytes(typ)
+    outs = [torch.empty(out_bytes, dtype=torch.uint8, device="cuda") for _ in range(min(copies, 4))]
+    stream = torch.cuda.current_stream()
+    im = None if (wl.imatrix is None or typ == gpuq.Q8_0) else wl.imatrix.data_ptr()
+
+    def launch(i):
+        got = gq.gpuq_requantize_dev(wl.src, raws[i % copies].data_ptr(), typ, outs[i % len(outs)].data_ptr(),
+                                     wl.nmat, wl.nrow, wl.ncol, im, stream.cuda_stream)
+        if got != out_bytes:
+            raise RuntimeError("gpuq_requantize_dev failed for %s" % gpuq.TYPE_NAMES[typ])
+
+    for i in range(warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(steps):
+        launch(warmup + i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    if gq.gpuq_take_error():
+        raise RuntimeError("a search reported no candidate (%s)" % gpuq.TYPE_NAMES[typ])
+    ms = e0.elapsed_time(e1) / steps
+    result = outs[(warmup + steps - 1) % len(outs)]
+    del raws[1:]
+    return ms, result
+
+
+def host_sample(torch, wl, rows):
+    """the first `rows` rows of every sampled matrix as host source bytes (the exact bytes the GPU read)"""
+    per_row = {0: 4, 30: 2}.get(wl.src)
+    if per_row is not None:
+        b = wl.raw.reshape(-1).view(torch.uint8)
+        return b[: rows * wl.ncol * per_row].cpu().numpy()
+    return wl.raw.reshape(-1)[: rows * wl.ncol // 32 * 17].cpu().numpy()
+
+
+def cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, wl, typ, ms, out_dev, sample_rows, want_cpu):
+    """the CPU baseline on a sample, the op count per weight, and a byte spot check of the GPU output"""
+    import numpy as np
+    nthr = cpu_threads()
+    raw = host_sample(torch, wl, sample_rows)
+    n = sample_rows * wl.ncol
+    im = None
+    if wl.imatrix is not None and typ != gpuq.Q8_0:
+        rows_per_mat = wl.nrow
+        nm = (sample_rows + rows_per_mat - 1) // rows_per_mat
+        im = wl.imatrix[:nm].cpu().numpy()
+    nmat_s, nrow_s = (sample_rows // wl.nrow, wl.nrow) if sample_rows >= wl.nrow else (1, sample_rows)
+    entry = {}
+    # byte spot check: the GPU's blocks of the sampled rows against the oracle's
+    rb = wl.ncol // gpuq.BLOCK[typ] * gq.gpuq_block_bytes(typ)
+    t0 = time.time()
+    want = orc.requantize_mt(wl.src, raw, typ, nmat_s, nrow_s, wl.ncol, im, unit_rows=16, nthreads=nthr)
+    cpu_s = time.time() - t0
+    got = out_dev[: sample_rows * rb].cpu().numpy()
+    entry["sample_identical_to_oracle"] = bool(np.array_equal(got, want))
+    if want_cpu:
+        entry["cpu_baseline"] = {"value": round(n / cpu_s / 1e6, 2), "unit": "Mweights/s", "cores": nthr,
+                                 "kind": "port",
+                                 "sample": "%d rows x %d of the same tensor (%.1f M weights), %.1f s on %d threads"
+                                           % (sample_rows, wl.ncol, n / 1e6, cpu_s, nthr)}
+    # roofline
+    n_total = wl.n
+    if typ == gpuq.Q8_0:
+        bpw = {0: 4.0, 30: 2.0}.get(wl.src, 17 / 32) + 34 / 32
+        achieved = bpw * n_total / (ms / 1e3) / 1e9
+        entry["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                             "algorithmic_bytes_per_weight": bpw}
+    else:
+        ops_rows = min(sample_rows, 64)
+        sub = raw[: (ops_rows * wl.ncol) * {0: 4, 30: 2}.get(wl.src, 0)] if wl.src in (0, 30) else \
+            raw[: ops_rows * wl.ncol // 32 * 17]
+        f = orc_ops.decode_src(wl.src, sub, ops_rows * wl.ncol).reshape(ops_rows, wl.ncol)
+        orc_ops.ops_read_reset()
+        orc_ops.quantize(typ, f, None if im is None else im[0])
+        opw = orc_ops.ops_read_reset() / (ops_rows * wl.ncol)
+        achieved = opw * n_total / (ms / 1e3) / 1e12
+        entry["roofline"] = {"bound": "valu", "achieved": round(achieved, 3), "peak": VALU_PEAK_TOPS,
+                             "unit": "Tops/s", "frac": round(achieved / VALU_PEAK_TOPS, 4), "traffic": None,
+                             "algorithmic_ops_per_weight": round(opw, 1)}
+    return entry
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--quick", action="store_true", help="headline workload only")
+    ap.add_argument("--experts", type=int, default=0, help="cap the expert count of the MoE workloads (profiling)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (experts would shard across GPUs with "
+              "no exchange step; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    torch.cuda.init()
+    import gpuq
+    from oracle import Oracle
+    gq = gpuq.load_gpuq(0)
+    orc = Oracle(tables=gpuq.tables_path())
+    orc_ops = Oracle("liboracle_ops.so", tables=gpuq.tables_path())
+
+    # headline: Q4_K with imatrix on the 2048 x 7168 BF16 tensor
+    c2 = wl_c2(torch, gpuq)
+    log("headline: Q4_K on %s" % c2.name)
+    ms, out = time_gpu(torch, gq, gpuq, c2, gpuq.Q4_K, args.steps, args.warmup)
+    head = cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, c2, gpuq.Q4_K, ms, out, c2.nrow, not args.no_cpu)
+    value = c2.n / (ms / 1e3) / 1e6
+    line = {"metric": METRIC, "value": round(value, 1), "unit": "Mweights/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "Q4_K with imatrix, " + c2.name, "type": "Q4_K", "shape": [2048, 7168],
+                       "source": "BF16", "entry_point": "gpuq_requantize_dev"},
+            "roofline": head["roofline"]}
+    if "cpu_baseline" in head:
+        line["cpu_baseline"] = head["cpu_baseline"]
+    line["sample_identical_to_oracle"] = head["sample_identical_to_oracle"]
+    per = {}
+    if not args.quick:
+        ksteps = max(1, min(args.steps, 5))
+        jobs = [("Q6_K", c2, gpuq.Q6_K, args.steps, c2.nrow)]
+        c1 = wl_c1(torch, gpuq)
+        jobs.insert(0, ("Q8_0", c1, gpuq.Q8_0, args.steps, c1.nrow))
+        for name, wl, typ, k, srows in jobs:
+            log("per type: %s on %s" % (name, wl.name))
+            ms_t, out_t = time_gpu(torch, gq, gpuq, wl, typ, k, args.warmup)
+            e = {"workload": wl.name, "value": round(wl.n / (ms_t / 1e3) / 1e6, 1), "unit": "Mweights/s",
+                 "ms_per_step": round(ms_t, 4), "steps": k}
+            e.update(cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, wl, typ, ms_t, out_t, srows, not args.no_cpu))
+            per[name] = e
+            del out_t
+        del c1
+        nthr = cpu_threads()
+        nexp_c3 = args.experts or 256
+        c3 = wl_c3(torch, gpuq, nexp_c3)
+        for name, typ in (("IQ2_XXS", gpuq.IQ2_XXS),):
+            log("per type: %s on %s" % (name, c3.name))
+            ms_t, out_t = time_gpu(torch, gq, gpuq, c3, typ, ksteps, 1)
+            e = {"workload": c3.name, "value": round(c3.n / (ms_t / 1e3) / 1e6, 1), "unit": "Mweights/s",
+                 "ms_per_step": round(ms_t, 3), "steps": ksteps}
+            srows = c3.nrow * min(nexp_c3, max(2, nthr))
+            e.update(cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, c3, typ, ms_t, out_t, srows, not args.no_cpu))
+            if "cpu_baseline" in e:
+                e["speedup_vs_cpu"] = round(e["value"] / e["cpu_baseline"]["value"], 1)
+            per[name] = e
+            del out_t
+        del c3
+        torch.cuda.empty_cache()
+        nexp_c4 = args.experts or 384
+        c4 = wl_c4(torch, gpuq, nexp_c4)
+        for name, typ in (("IQ1_S", gpuq.IQ1_S), ("IQ1_M", gpuq.IQ1_M)):
+            log("per type: %s on %s" % (name, c4.name))
+            ms_t, out_t = time_gpu(torch, gq, gpuq, c4, typ, ksteps, 1)
+            e = {"workload": c4.name, "value": round(c4.n / (ms_t / 1e3) / 1e6, 1), "unit": "Mweights/s",
+                 "ms_per_step": round(ms_t, 3), "steps": ksteps}
+            srows = c4.nrow * min(nexp_c4, max(2, nthr))
+            e.update(cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, c4, typ, ms_t, out_t, srows, not args.no_cpu))
+            if "cpu_baseline" in e:
+                e["speedup_vs_cpu"] = round(e["value"] / e["cpu_baseline"]["value"], 1)
+            per[name] = e
+            del out_t
+        del c4
+        line["per_type"] = per
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
