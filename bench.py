@@ -97,6 +97,93 @@ def wl_c4(torch, gpuq, nexp=384):
                     "log-normal(0,1.5) imatrix" % nexp, gpuq.MXFP4, nexp, 2048, 7168, raw.reshape(-1), im)
 
 
+def wl_c5(torch, gpuq, ldlq, nexp=64, ncal=8192):
+    """64 BF16 experts of 2048 x 7168, N(0, 0.02); each with its own SPD Hessian H = X^T X / n + 1e-2 mean(diag) I
+    from X [8192 x 7168] of Student-t (nu = 4) activations, factored with prepare_hessian(H, n=1, damp=0.01, seq)
+    and a log-normal(0, 1.5) imatrix (IQ2_S needs one)"""
+    ne1, ne0 = 2048, 7168
+    g = torch.Generator(device="cuda").manual_seed(5)
+    W = (torch.randn((nexp, ne1, ne0), device="cuda", generator=g) * 0.02).to(torch.bfloat16).float().contiguous()
+    Us = torch.empty((nexp, ne0, ne0), dtype=torch.float64, device="cuda")
+    perm = None
+    for e in range(nexp):
+        z = torch.randn((ncal, ne0), device="cuda", generator=g)
+        chi = (torch.randn((4, ncal, ne0), device="cuda", generator=g) ** 2).sum(0) / 4
+        X = z / torch.sqrt(chi)
+        H = (X.T @ X).double() / ncal
+        H.diagonal().add_(1e-2 * float(torch.diagonal(H).mean()))
+        U, perm, _, _ = ldlq.prepare_hessian_torch(H, 1, damp=0.01, order="seq")
+        Us[e] = U
+        del z, chi, X, H, U
+    im = torch.exp(torch.randn(nexp, ne0, device="cuda", generator=g) * 1.5).contiguous()
+    return W, Us, perm, im
+
+
+def bench_ldlq(torch, gq, gpuq, orc, steps, want_cpu, nexp):
+    """IQ2_S with LDLQ error feedback over 64 experts; one step = the whole loop (gpuq_ldlq_dev)"""
+    import numpy as np
+    from gpuq import ldlq
+    t0 = time.time()
+    W, Us, perm, im = wl_c5(torch, gpuq, ldlq, nexp)
+    log("LDLQ workload ready in %.1f s" % (time.time() - t0))
+    nexp_, ne1, ne0 = W.shape
+    slots = np.ascontiguousarray(ldlq.slot_order(perm), dtype=np.int64)
+    pt = torch.as_tensor(perm, device="cuda")
+    Wp0 = W.index_select(2, pt).contiguous()
+    qw = im.index_select(1, pt).contiguous()
+    tsize = gq.gpuq_block_bytes(gpuq.IQ2_S)
+    out = torch.empty((nexp_, ne1, ne0 // 256 * tsize), dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream()
+    times = []
+    for it in range(steps + 1):
+        Wp = Wp0.clone()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        got = gq.gpuq_ldlq_dev(gpuq.IQ2_S, Wp.data_ptr(), Us.data_ptr(), ne0 * ne0, qw.data_ptr(), nexp_, ne1, ne0,
+                               slots.ctypes.data, 1, out.data_ptr(), stream.cuda_stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        if got != out.numel():
+            raise RuntimeError("gpuq_ldlq_dev failed")
+        if it:                                            # (the first call is the warm-up)
+            times.append(e0.elapsed_time(e1))
+        del Wp
+    ms = sum(times) / len(times)
+    n = nexp_ * ne1 * ne0
+    flops = 2.0 * nexp_ * ne1 * 256 * sum(ne0 - 256 * (k + 1) for k in range(ne0 // 256))
+    e = {"workload": "IQ2_S with LDLQ error feedback (seq order, imatrix weights), %d BF16 experts of 2048x7168, "
+                     "per-expert H from 8192 Student-t(4) activations" % nexp_,
+         "value": round(n / (ms / 1e3) / 1e6, 1), "unit": "Mweights/s", "ms_per_step": round(ms, 2),
+         "steps": steps,
+         "roofline": {"bound": "fp64", "achieved": round(flops / (ms / 1e3) / 1e12, 2), "peak": 78.6,
+                      "unit": "TFLOP/s", "frac": round(flops / (ms / 1e3) / 1e12 / 78.6, 4), "traffic": None,
+                      "algorithmic_flops_per_step": flops, "note": "whole loop time (quantize + solve + update)"}}
+    # CPU leg and spot check: rows are independent in the loop, so a row sample of expert 0 is exact
+    rows = 16 * max(1, cpu_threads() // 4)
+    U0 = Us[0].cpu().numpy()
+    Wp_s = Wp0[0:1, :rows].cpu().numpy()
+    qw0 = qw[0:1].cpu().numpy()
+    nthr = cpu_threads()
+    per = max(1, rows // nthr)
+    import concurrent.futures
+    t0 = time.time()
+    with concurrent.futures.ThreadPoolExecutor(nthr) as ex:
+        parts = list(ex.map(lambda r0: orc.ldlq(gpuq.IQ2_S, Wp_s[:, r0:r0 + per], U0, qw0, slots)[0],
+                            range(0, rows, per)))
+    cpu_s = time.time() - t0
+    want = np.concatenate(parts, axis=1)
+    e["sample_identical_to_oracle"] = bool(np.array_equal(out[0:1, :rows].cpu().numpy(), want))
+    if want_cpu:
+        e["cpu_baseline"] = {"value": round(rows * ne0 / cpu_s / 1e6, 3), "unit": "Mweights/s", "cores": nthr,
+                             "kind": "port", "sample": "%d rows of expert 0 (their LDLQ is independent of the other "
+                                                       "rows), %.1f s on %d threads" % (rows, cpu_s, nthr)}
+        e["speedup_vs_cpu"] = round(e["value"] / e["cpu_baseline"]["value"], 1)
+    del W, Us, Wp0, out
+    torch.cuda.empty_cache()
+    return e
+
+
 def time_gpu(torch, gq, gpuq, wl, typ, steps, warmup):
     """average kernel time (ms) of gpuq_requantize_dev over `steps` launches, HIP events on the launch stream"""
     bpw = {gpuq.F32: 4.0, gpuq.BF16: 2.0, gpuq.MXFP4: 17 / 32}[wl.src]
@@ -271,6 +358,10 @@ def main():
             per[name] = e
             del out_t
         del c4
+        torch.cuda.empty_cache()
+        log("per type: IQ2_S LDLQ")
+        per["IQ2_S_LDLQ"] = bench_ldlq(torch, gq, gpuq, orc, min(args.steps, 2), not args.no_cpu,
+                                       args.experts or 64)
         line["per_type"] = per
     print(json.dumps(line), flush=True)
 

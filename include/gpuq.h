@@ -77,6 +77,16 @@ size_t gpuq_dequantize_src_dev(int src_type, const void *d_raw, float *d_out, in
 size_t gpuq_requantize_dev(int src_type, const void *d_raw, int type, void *d_dst, int64_t nmat, int64_t nrow,
                            int64_t n_per_row, const float *d_imatrix, void *stream);
 
+/* The LDLQ error-feedback loop on the device, for nmat matrices that share (u_stride = 0) or own (u_stride =
+ * ne0*ne0) a factor U: replaces the loop of tools/ldlq.py:391-431 (quantize_matrix_torch), which calls
+ * gpuq_quantize_dev / gpuq_dequantize_dev per block and solves / updates in torch. d_wp [nmat][ne1][ne0] f32 in
+ * permuted column order (updated in place), d_u [ne0][ne0] f64 row-major upper factor of the permuted inverse
+ * Hessian, d_qw [nmat][ne0] f32 importances in permuted order, blk_order (host) the output slot of each permuted
+ * 256-column block, d_out [nmat][ne1][ne0/256 blocks]. The f64 solve and update use fixed-order FMA chains (the CPU
+ * oracle computes the same ones). Types: the i-quants with a dequantizer grid and IQ4_XS. Asynchronous. */
+size_t gpuq_ldlq_dev(int type, float *d_wp, const double *d_u, int64_t u_stride, const float *d_qw, int64_t nmat,
+                     int64_t ne1, int64_t ne0, const int64_t *blk_order, int feedback, void *d_out, void *stream);
+
 /* Reads and clears the flag the kernels set where the reference would trap (a key with no candidate point: non-
  * finite input or an inconsistent table). Synchronizes the device. */
 int gpuq_take_error(void);

@@ -7,7 +7,7 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PKG = os.path.join(ROOT, "trench-gguf_amd")
-for p in (os.path.join(ROOT, "oracle"), PKG, os.path.join(PKG, "gpuq")):
+for p in (os.path.join(ROOT, "oracle"), os.path.join(PKG, "gpuq"), PKG):
     if p not in sys.path:
         sys.path.insert(0, p)
 

@@ -1,0 +1,82 @@
+"""The on-device LDLQ loop (gpuq_ldlq_dev) against the CPU oracle's fixed-order loop, byte for byte, on the recipe
+of the reference's tools/test_ldlq.py:42-50 (a correlated Gaussian design, H = X^T X in f64, imatrix = diag(H)/n,
+W ~ N(0, 0.05)), in sequential and act order, with a shared and with per-matrix factors, and without feedback
+(where it must equal plain quantization, tools/test_ldlq.py:69-73)."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TYPES = {22: "iq2_s", 16: "iq2_xxs", 19: "iq1_s", 29: "iq1_m", 23: "iq4_xs", 18: "iq3_xxs"}
+
+
+@pytest.fixture(scope="module")
+def env():
+    import torch
+    torch.cuda.init()
+    import gpuq
+    return torch, gpuq, gpuq.load_gpuq(0)
+
+
+def design(ne1=64, ne0=1024, seed=1):
+    rng = np.random.default_rng(seed)
+    n = 4 * ne0
+    A = rng.standard_normal((ne0, ne0)).astype(np.float32) * 0.2 + np.eye(ne0, dtype=np.float32)
+    X = rng.standard_normal((n, ne0)).astype(np.float32) @ A
+    X *= (1 + 3 * rng.random(ne0, dtype=np.float32))[None]
+    H = (X.T @ X).astype(np.float64)
+    imatrix = (np.diag(H) / n).astype(np.float32)
+    W = (rng.standard_normal((2, ne1, ne0)) * 0.05).astype(np.float32)
+    return H, n, imatrix, W
+
+
+@pytest.mark.parametrize("order", ["seq", "act"])
+@pytest.mark.parametrize("typ", list(TYPES), ids=list(TYPES.values()))
+def test_ldlq_matches_oracle(env, oracle_lib, typ, order):
+    torch, gpuq, gq = env
+    from gpuq import ldlq
+    H, n, imatrix, W = design()
+    U, perm, diag_n, _ = ldlq.prepare_hessian(H, n, damp=0.01, order=order)
+    qw = np.stack([ldlq.block_weights("imatrix", perm=perm, imatrix=imatrix)] * 2)
+    slots = ldlq.slot_order(perm)
+    want, want_w = oracle_lib.ldlq(typ, W[:, :, perm], U, qw, slots, feedback=True)
+    print("case ldlq %s %s" % (TYPES[typ], order), flush=True)
+    Wd = torch.from_numpy(W).cuda()
+    got = ldlq.quantize_matrix_dev(gq, typ, Wd, torch.from_numpy(U).cuda(), perm, torch.from_numpy(qw).cuda())
+    torch.cuda.synchronize()
+    g = got.cpu().numpy()
+    bb = gq.gpuq_block_bytes(typ)
+    same = (g.reshape(-1, bb) == want.reshape(-1, bb)).all(axis=1)
+    assert same.all(), "%d of %d blocks differ" % (int((~same).sum()), len(same))
+    assert gq.gpuq_take_error() == 0
+
+
+def test_ldlq_per_matrix_factors(env, oracle_lib):
+    torch, gpuq, gq = env
+    from gpuq import ldlq
+    H, n, imatrix, W = design(ne1=32, ne0=768)
+    H2, n2, _, _ = design(ne1=32, ne0=768, seed=2)
+    U1, perm, _, _ = ldlq.prepare_hessian(H, n)
+    U2, _, _, _ = ldlq.prepare_hessian(H2, n2)
+    qw = np.stack([imatrix, imatrix * 0.5]).astype(np.float32)
+    slots = ldlq.slot_order(perm)
+    want = np.concatenate([oracle_lib.ldlq(22, W[m:m + 1], U, qw[m:m + 1], slots)[0] for m, U in ((0, U1), (1, U2))])
+    Us = torch.from_numpy(np.stack([U1, U2])).cuda()
+    got = ldlq.quantize_matrix_dev(gq, 22, torch.from_numpy(W).cuda(), Us, perm, torch.from_numpy(qw).cuda(),
+                                   u_per_matrix=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy(), want)
+
+
+def test_ldlq_without_feedback_is_plain_quantization(env, oracle_lib):
+    torch, gpuq, gq = env
+    from gpuq import ldlq
+    H, n, imatrix, W = design()
+    U, perm, _, _ = ldlq.prepare_hessian(H, n)
+    qw = np.stack([imatrix] * 2)
+    got = ldlq.quantize_matrix_dev(gq, 16, torch.from_numpy(W).cuda(), torch.from_numpy(U).cuda(), perm,
+                                   torch.from_numpy(qw).cuda(), feedback=False)
+    torch.cuda.synchronize()
+    for m in range(2):
+        want = oracle_lib.quantize(16, W[m], imatrix)            # one whole-row call, tools/test_ldlq.py:69-73
+        assert np.array_equal(got[m].cpu().numpy(), want)

@@ -28,6 +28,10 @@ struct QParams {
     const int32_t *map3;
     int grid_size, map_size, neigh_len;
     int *err;               // set when a search finds no candidate (the reference traps there)
+    // strided views (the LDLQ loop quantizes one block column of every row): unit b reads its weights at element
+    // b*sb_stride + sb_off, its importance at row*qw_stride + qw_off, and writes its block at byte
+    // b*out_stride + out_off. The contiguous defaults are sb_stride = BS, qw_stride = BS, out_stride = BB, 0 offsets.
+    int64_t sb_stride, sb_off, qw_stride, qw_off, out_stride, out_off;
 };
 
 DEV int64_t qw_row(const QParams &p, int64_t b) { return (b / p.qw_mat) * p.qw_mod + (b % p.qw_mod) / p.qw_div; }
@@ -109,11 +113,17 @@ __global__ __launch_bounds__(WG_THREADS) void k_quant(QParams p) {
         img_zero(img, img_bytes<T>());
         wave_sync();
         float x[T::N];
-        SrcLoad<SRC, T::N>::load(p.src, b * T::BS + g * T::N, x);
-        const float *qw = p.qw ? p.qw + qw_row(p, b) * T::BS + g * T::N : nullptr;
+        SrcLoad<SRC, T::N>::load(p.src, b * p.sb_stride + p.sb_off + g * T::N, x);
+        const float *qw = p.qw ? p.qw + qw_row(p, b) * p.qw_stride + p.qw_off + g * T::N : nullptr;
         T::quant(x, qw, g, img, slot * T::BB, lds, p);
         wave_sync();
-        img_store(p.dst + b0 * T::BB, img, nact * T::BB);
+        if (p.out_stride == T::BB && p.out_off == 0) {
+            img_store(p.dst + b0 * T::BB, img, nact * T::BB);
+        } else if (slot < nact) {         // strided: each group copies its own block, 16 bits a lane
+            uint16_t *o = (uint16_t *)(p.dst + b * p.out_stride + p.out_off);
+            const uint16_t *s = (const uint16_t *)(img + slot * T::BB);
+            for (int h = g; h < T::BB / 2; h += T::G) o[h] = s[h];
+        }
         wave_sync();
     }
 }

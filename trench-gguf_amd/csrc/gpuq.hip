@@ -18,6 +18,7 @@
 #include "iq1.cuh"
 #include "iq3.cuh"
 #include "dequant.cuh"
+#include "ldlq.cuh"
 
 extern "C" size_t gpuq_block_bytes(int type);
 
@@ -53,7 +54,7 @@ struct Buf {
         return true;
     }
 };
-Buf g_raw, g_qw, g_out, g_f32;
+Buf g_raw, g_qw, g_out, g_f32, g_es;
 
 bool is_search_type(int t) {
     return t == T_IQ2_XXS || t == T_IQ2_XS || t == T_IQ2_S || t == T_IQ1_S || t == T_IQ3_XXS || t == T_IQ3_S;
@@ -232,6 +233,12 @@ QParams params_for(int type, const void *src, void *dst, int64_t nunits, const f
     p.map_size = t.map_size;
     p.neigh_len = t.neigh_len;
     p.err = g_err;
+    p.sb_stride = block_len(type);
+    p.sb_off = 0;
+    p.qw_stride = block_len(type);
+    p.qw_off = 0;
+    p.out_stride = (int64_t)gpuq_block_bytes(type);
+    p.out_off = 0;
     return p;
 }
 
@@ -276,6 +283,32 @@ size_t quantize_host(int src, const void *raw, int type, void *dst, int64_t nmat
     if (hipMemcpy(&err, g_err, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess || err) return 0;
     if (hipMemcpy(dst, g_out.p, out_bytes, hipMemcpyDeviceToHost) != hipSuccess) return 0;
     return out_bytes;
+}
+
+bool ldlq_type(int t) {
+    return t == T_IQ2_XXS || t == T_IQ2_XS || t == T_IQ2_S || t == T_IQ3_XXS || t == T_IQ3_S || t == T_IQ1_S ||
+           t == T_IQ1_M || t == T_IQ4_XS;
+}
+
+bool launch_solve(int type, const float *W, const uint8_t *q, int64_t q_stride, int64_t q_off, const double *U,
+                  int64_t u_stride, int64_t nmat, int64_t ne1, int64_t ne0, int64_t c0, double *Es, hipStream_t st) {
+    const dim3 grid((unsigned)((ne1 + 63) / 64), (unsigned)nmat);
+    const uint64_t *dq = tab_of(type).dq;
+#define KSOLVE(T) hipLaunchKernelGGL((k_ldlq_solve<T>), grid, dim3(64), 0, st, W, q, q_stride, q_off, U, u_stride, \
+                                     ne1, ne0, c0, Es, dq)
+    switch (type) {
+        case T_IQ2_XXS: KSOLVE(T_IQ2_XXS); break;
+        case T_IQ2_XS: KSOLVE(T_IQ2_XS); break;
+        case T_IQ2_S: KSOLVE(T_IQ2_S); break;
+        case T_IQ3_XXS: KSOLVE(T_IQ3_XXS); break;
+        case T_IQ3_S: KSOLVE(T_IQ3_S); break;
+        case T_IQ1_S: KSOLVE(T_IQ1_S); break;
+        case T_IQ1_M: KSOLVE(T_IQ1_M); break;
+        case T_IQ4_XS: KSOLVE(T_IQ4_XS); break;
+        default: return false;
+    }
+#undef KSOLVE
+    return hipGetLastError() == hipSuccess;
 }
 
 }  // namespace
@@ -462,4 +495,47 @@ extern "C" int gpuq_take_error(void) {
     if (hipMemcpy(&err, g_err, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess) return 1;
     (void)hipMemset(g_err, 0, sizeof(int));
     return err;
+}
+
+// The LDLQ error-feedback loop on the device (tools/ldlq.py:71-107 quantize_matrix / 391-431 quantize_matrix_torch;
+// no single counterpart symbol in the reference, which drives gpuq_quantize_dev / gpuq_dequantize_dev and torch from
+// Python). d_wp: nmat matrices [ne1][ne0] f32 in permuted column order, updated in place; d_u: the upper Cholesky
+// factor of the permuted inverse Hessian, [ne0][ne0] f64 row-major, matrix m's at d_u + m*u_stride (0: shared);
+// d_qw: [nmat][ne0] f32 importances in permuted order; blk_order (host, ne0/256 entries): the output slot of permuted
+// block k; d_out: [nmat][ne1][ne0/256 blocks]. feedback = 0 quantizes every block as is. Asynchronous on `stream`.
+extern "C" size_t gpuq_ldlq_dev(int type, float *d_wp, const double *d_u, int64_t u_stride, const float *d_qw,
+                                int64_t nmat, int64_t ne1, int64_t ne0, const int64_t *blk_order, int feedback,
+                                void *d_out, void *stream) {
+    if (!ldlq_type(type) || !gpuq_can_dequantize_type(type) || !type_ok(type, ne0, d_qw != nullptr)) return 0;
+    if (nmat <= 0 || ne1 <= 0 || ne0 <= 0 || ne0 % QK || u_stride < 0 || !blk_order) return 0;
+    if (((uintptr_t)d_wp & 15) || (d_qw && ((uintptr_t)d_qw & 15)) || ((uintptr_t)d_u & 7) || ((uintptr_t)d_out & 1))
+        return 0;
+    const int64_t nblk = ne0 / QK;
+    for (int64_t k = 0; k < nblk; ++k)
+        if (blk_order[k] < 0 || blk_order[k] >= nblk) return 0;
+    const hipStream_t st = (hipStream_t)stream;
+    const int64_t bb = (int64_t)gpuq_block_bytes(type), rows = nmat * ne1;
+    std::lock_guard<std::mutex> lock(g_mu);
+    if (feedback && nblk > 1 && !g_es.grow((size_t)rows * QK * 8)) return 0;
+    for (int64_t k = 0; k < nblk; ++k) {
+        const int64_t c0 = k * QK;
+        QParams p = params_for(type, d_wp, d_out, rows, d_qw, ne1, 1, 1);
+        p.sb_stride = ne0;
+        p.sb_off = c0;
+        p.qw_stride = ne0;
+        p.qw_off = c0;
+        p.out_stride = nblk * bb;
+        p.out_off = blk_order[k] * bb;
+        if (!dispatch(type, T_F32, p, st)) return 0;
+        if (!feedback || k + 1 >= nblk) continue;
+        if (!launch_solve(type, d_wp, (const uint8_t *)d_out, nblk * bb, blk_order[k] * bb, d_u, u_stride, nmat, ne1,
+                          ne0, c0, (double *)g_es.p, st))
+            return 0;
+        const dim3 ug((unsigned)((ne0 - c0 - QK + LDLQ_TN - 1) / LDLQ_TN), (unsigned)((ne1 + LDLQ_TM - 1) / LDLQ_TM),
+                      (unsigned)nmat);
+        hipLaunchKernelGGL(k_ldlq_update, ug, dim3(256), 0, st, d_wp, (const double *)g_es.p, d_u, u_stride, ne1, ne0,
+                           c0);
+        if (hipGetLastError() != hipSuccess) return 0;
+    }
+    return (size_t)(rows * nblk * bb);
 }

@@ -1,0 +1,121 @@
+// trench-gguf_amd/csrc/ldlq.cuh - the LDLQ error-feedback loop on the device (tools/ldlq.py:71-107, 391-431).
+//
+// For column block k (256 permuted columns, c0 = 256k) of nmat matrices of ne1 rows:
+//   1. the quantizer runs on the strided view of block k of every row (frame.cuh) and writes each row's block
+//      into its output slot;
+//   2. k_ldlq_solve, one lane a row: E = blk - to_float(block bytes) in f32, then Es = E U_BB^-1 by forward
+//      substitution in f64: Es[j] = (E[j] - sum_{i<j} Es[i] U[c0+i][c0+j]) / U[c0+j][c0+j], each sum a fused
+//      multiply-add chain over i in ascending order;
+//   3. k_ldlq_update, a register-tiled f64 GEMM: W[r][c] -= (float)(sum_{i<256} Es[r][i] U[c0+i][c]) for the later
+//      columns c, each output a fused multiply-add chain over i in ascending order from 0.0.
+// The reference leaves the order of those sums to LAPACK / BLAS (numpy's LU solve, torch's solve_triangular and
+// GEMM); this library fixes it as above, and its CPU oracle computes the same chains, so the bytes are reproducible
+// on any hardware. The f64 work runs on VALU v_fma_f64, whose rate on gfx950 equals the f64 MFMA peak.
+#pragma once
+#include "dequant.cuh"
+
+#define LDLQ_BK 16            // k-chunk of the update GEMM
+#define LDLQ_TM 128           // update tile rows
+#define LDLQ_TN 128           // update tile columns
+
+// one wave = 64 rows of one matrix (blockIdx.y), so U's addresses are wave-uniform (scalar loads)
+template <int TYPE>
+__global__ __launch_bounds__(64) void k_ldlq_solve(const float *__restrict__ W, const uint8_t *__restrict__ q,
+                                                   int64_t q_stride, int64_t q_off, const double *__restrict__ U,
+                                                   int64_t u_stride, int64_t ne1, int64_t ne0, int64_t c0,
+                                                   double *__restrict__ Es, const uint64_t *__restrict__ grid) {
+    const int64_t m = blockIdx.y;
+    const int64_t row = (int64_t)blockIdx.x * 64 + threadIdx.x;
+    const bool live = row < ne1;
+    const int64_t r = m * ne1 + (live ? row : ne1 - 1);
+    const double *Um = U + m * u_stride;
+    const float *wrow = W + r * ne0 + c0;
+    const uint8_t *qb = q + r * q_stride + q_off;
+    double *es = Es + r * QK;
+    for (int c = 0; c < 8; ++c) {
+        float y[32];
+        dq_chunk<TYPE>(qb, c, y, grid);
+        double acc[32];
+        const float4 *wp = (const float4 *)(wrow + 32 * c);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const float4 v = wp[t];
+            acc[4 * t + 0] = (double)(v.x - y[4 * t + 0]);
+            acc[4 * t + 1] = (double)(v.y - y[4 * t + 1]);
+            acc[4 * t + 2] = (double)(v.z - y[4 * t + 2]);
+            acc[4 * t + 3] = (double)(v.w - y[4 * t + 3]);
+        }
+        for (int i = 0; i < 32 * c; ++i) {
+            const double e = es[i];
+            const double *urow = Um + (c0 + i) * ne0 + c0 + 32 * c;
+#pragma unroll
+            for (int t = 0; t < 32; ++t) acc[t] = fma(-e, urow[t], acc[t]);
+        }
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            const double *urow = Um + (c0 + 32 * c + i) * ne0 + c0 + 32 * c;
+            const double v = acc[i] / urow[i];
+            if (live) es[32 * c + i] = v;
+#pragma unroll
+            for (int t = i + 1; t < 32; ++t) acc[t] = fma(-v, urow[t], acc[t]);
+        }
+    }
+}
+
+// W[m][row][c] -= (float)(Es[m*ne1+row][:] . U_m[c0 .. c0+255][c]) for c in [c0 + 256, ne0)
+__global__ __launch_bounds__(256) void k_ldlq_update(float *__restrict__ W, const double *__restrict__ Es,
+                                                     const double *__restrict__ U, int64_t u_stride, int64_t ne1,
+                                                     int64_t ne0, int64_t c0) {
+    __shared__ __align__(16) double As[LDLQ_BK][LDLQ_TM + 2];
+    __shared__ __align__(16) double Bs[LDLQ_BK][LDLQ_TN + 2];
+    const int64_t m = blockIdx.z;
+    const int64_t row0 = (int64_t)blockIdx.y * LDLQ_TM;
+    const int64_t col0 = c0 + QK + (int64_t)blockIdx.x * LDLQ_TN;
+    const double *Um = U + m * u_stride;
+    const int tid = threadIdx.x, tx = tid % 16, ty = tid / 16;
+    double acc[8][8];
+#pragma unroll
+    for (int a = 0; a < 8; ++a)
+#pragma unroll
+        for (int b = 0; b < 8; ++b) acc[a][b] = 0.0;
+    // loader roles: A: row tid/2, k half (tid%2)*8; B: k row tid/16, columns 8*(tid%16)
+    const int ar = tid / 2, ak = (tid % 2) * 8;
+    const int bk = tid / 16, bc = 8 * (tid % 16);
+    const bool a_ok = row0 + ar < ne1;
+    const double *arow = Es + (m * ne1 + (a_ok ? row0 + ar : 0)) * QK;
+    for (int k0 = 0; k0 < QK; k0 += LDLQ_BK) {
+        double av[8], bv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) av[j] = a_ok ? arow[k0 + ak + j] : 0.0;
+        const double *brow = Um + (c0 + k0 + bk) * ne0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) bv[j] = col0 + bc + j < ne0 ? brow[col0 + bc + j] : 0.0;
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 8; ++j) As[ak + j][ar] = av[j];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) Bs[bk][bc + j] = bv[j];
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < LDLQ_BK; ++kk) {
+            double a[8], b[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) { a[j] = As[kk][8 * ty + j]; b[j] = Bs[kk][8 * tx + j]; }
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[i][j] = fma(a[i], b[j], acc[i][j]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int64_t row = row0 + 8 * ty + i;
+        if (row >= ne1) continue;
+        float *wr = W + (m * ne1 + row) * ne0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int64_t col = col0 + 8 * tx + j;
+            if (col < ne0) wr[col] = wr[col] - (float)acc[i][j];
+        }
+    }
+}

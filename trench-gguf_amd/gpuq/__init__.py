@@ -37,6 +37,7 @@ SIGNATURES = {
     "gpuq_dequantize_src_dev": (_sz, [_i, _vp, _vp, _i64, _vp]),
     "gpuq_requantize_dev": (_sz, [_i, _vp, _i, _vp, _i64, _i64, _i64, _vp, _vp]),
     "gpuq_take_error": (_i, []),
+    "gpuq_ldlq_dev": (_sz, [_i, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp, _i, _vp, _vp]),
 }
 REFERENCE_SYMBOLS = list(SIGNATURES)[:12]
 
