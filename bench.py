@@ -287,8 +287,8 @@ def main():
     ap.add_argument("--experts", type=int, default=0, help="cap the expert count of the MoE workloads (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (experts would shard across GPUs with "
-              "no exchange step; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU: there is no multi-GPU path (experts would shard across GPUs with no "
+              "exchange step, each GPU writing disjoint byte ranges). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     import torch
     torch.cuda.init()

@@ -31,8 +31,9 @@
 #define EPS_IQ3XXS 1e-8f
 #define DELTA_IQ1 0.125f
 #define NGRID_IQ1 2048
-#define GMAX(a, b) ((a) > (b) ? (a) : (b))
-#define GMIN(a, b) ((a) < (b) ? (a) : (b))
+/* ggml's MAX / MIN (a > b ? a : b) with each argument evaluated once */
+#define GMAX(a, b) ({ __typeof__(a) ga_ = (a); __typeof__(b) gb_ = (b); ga_ > gb_ ? ga_ : gb_; })
+#define GMIN(a, b) ({ __typeof__(a) ga_ = (a); __typeof__(b) gb_ = (b); ga_ < gb_ ? ga_ : gb_; })
 
 #ifdef GQO_COUNT_OPS
 static __thread uint64_t t_ops;
@@ -68,7 +69,7 @@ static uint16_t f32_to_f16(float f) {
     base = float_of((bias >> 1) + 0x07800000u) + base;
     const uint32_t b = bits_of(base);
     const uint32_t nonsign = ((b >> 13) & 0x00007C00u) + (b & 0x00000FFFu);
-    OPS(14);
+    OPS(12);
     return (uint16_t)((sgn >> 16) | (w2 > 0xFF000000u ? 0x7E00u : nonsign));
 }
 
@@ -89,7 +90,7 @@ static float f16_to_f32(uint16_t h) {
 /* round half to even for |v| < 2^22 via the fp32 adder (gpuq/gpuq.hip:108-112) */
 static inline int near_int(float v) {
     const float t = v + 12582912.f;
-    OPS(3);
+    OPS(2);
     return (int)(bits_of(t) & 0x007fffffu) - 0x00400000;
 }
 
@@ -183,7 +184,7 @@ static float qp_levels(int n, int nmax, const float *x, uint8_t *L, const float 
         const float diff = x[i] - scale * L[i];
         best_mse += qw[i] * diff * diff;
     }
-    OPS(2 * C_DIV + 2 * n + 6 * n);
+    OPS(2 * C_DIV + n + 6 * n);
     for (int is = -4; is <= 4; ++is) {
         if (is == 0) continue;
         const float iscale_is = (0.1f * is + nmax) / mx;
@@ -195,7 +196,7 @@ static float qp_levels(int n, int nmax, const float *x, uint8_t *L, const float 
             const float diff = x[i] - scale_is * l;
             mse += qw[i] * diff * diff;
         }
-        OPS(4 + 2 * C_DIV + n * 9 + 1);
+        OPS(3 + 2 * C_DIV + n * 8 + 1);
         if (mse < best_mse) { best_mse = mse; iscale = iscale_is; }
     }
     float sumlx = 0, suml2 = 0;
@@ -206,14 +207,14 @@ static float qp_levels(int n, int nmax, const float *x, uint8_t *L, const float 
         sumlx += qw[i] * x[i] * l;
         suml2 += qw[i] * l * l;
     }
-    OPS(n * 10);
+    OPS(n * 9);
     for (int pass = 0; pass < 5; ++pass) {
         int changed = 0;
         for (int i = 0; i < n; ++i) {
             const float w = qw[i];
             float slx = sumlx - w * x[i] * L[i];
             float sl2 = suml2 - w * L[i] * L[i];
-            OPS(10);
+            OPS(8);
             if (slx > 0 && sl2 > 0) {
                 int nl = near_int(x[i] * sl2 / slx);
                 nl = GMIN(nmax, nl);
@@ -221,7 +222,7 @@ static float qp_levels(int n, int nmax, const float *x, uint8_t *L, const float 
                 if (nl != L[i]) {
                     slx += w * x[i] * nl;
                     sl2 += w * nl * nl;
-                    OPS(16);
+                    OPS(11);
                     if (slx * slx * suml2 > sumlx * sumlx * sl2) {
                         L[i] = (uint8_t)nl; sumlx = slx; suml2 = sl2;
                         ++changed;
@@ -248,7 +249,7 @@ static int nb_iq2(const otab *t, const uint16_t *nb, const float *xv, const floa
             const float diff = scale * q - xv[i];
             d2 += wa[i] * diff * diff;
         }
-        OPS(8 * 6 + 2);
+        OPS(8 * 6 + 3);
         if (d2 < best) { best = d2; gi = nb[j]; }
     }
     if (gi < 0) { t_err = 1; gi = 0; }
@@ -349,7 +350,7 @@ static float sum_sq(const float *x, int n) {
 
 static void iq_weights(const float *qw, const float *xb, float sigma2, float *weight, int n) {
     for (int i = 0; i < n; ++i) weight[i] = qw[i] * sqrtf(sigma2 + xb[i] * xb[i]);
-    OPS(n * (3 + C_SQRT));
+    OPS(n * (2 + C_SQRT));
 }
 
 /* ------------------------------------------------------------------ IQ2_XXS (gpuq/gpuq.hip:245-387) */
@@ -371,7 +372,7 @@ static void o_iq2_xxs(const float *xbl, const float *qwbl, uint8_t *y, const ota
         for (int k = 0; k < 4; ++k) bsg[k] = signs_even(xb + 8 * k, weight + 8 * k, xval + 8 * k);
         float mx = xval[0];
         for (int i = 1; i < 32; ++i) mx = GMAX(mx, xval[i]);
-        OPS(32);
+        OPS(32 + 32);
         if (mx < EPS_GROUP) {
             scales[ib] = 0;
             memset(L, 0, sizeof L);
@@ -396,7 +397,7 @@ static void o_iq2_xxs(const float *xbl, const float *qwbl, uint8_t *y, const ota
                     Laux[8 * k + i] = (int8_t)GMAX(0, GMIN(kMaxQ - 1, l));
                     u |= Laux[8 * k + i] << 2 * i;
                 }
-                OPS(8 * 7 + 1);
+                OPS(8 * 5 + 1);
                 const int m = map_at(t, u);
                 if (m < 0) nb_iq2(t, neigh_at(t, m), xval + 8 * k, waux + 8 * k, this_scale, Laux + 8 * k);
             }
@@ -407,7 +408,7 @@ static void o_iq2_xxs(const float *xbl, const float *qwbl, uint8_t *y, const ota
                 sumqx += w * xval[i] * q;
                 sumq2 += w * q * q;
             }
-            OPS(32 * 7 + 5);
+            OPS(32 * 6 + 5);
             if (sumq2 > 0 && sumqx * sumqx > best * sumq2) {
                 scale = sumqx / sumq2;
                 best = scale * sumqx;
@@ -424,7 +425,7 @@ static void o_iq2_xxs(const float *xbl, const float *qwbl, uint8_t *y, const ota
                     l = GMAX(0, GMIN(kMaxQ - 1, l));
                     u |= l << 2 * i;
                 }
-                OPS(8 * 7);
+                OPS(8 * 5);
                 int gi = map_at(t, u);
                 if (gi < 0) gi = nb_iq2(t, neigh_at(t, gi), xval + 8 * k, waux + 8 * k, scale, L + 8 * k);
                 const int8_t *pg = grid_pt(t, gi);
@@ -437,7 +438,7 @@ static void o_iq2_xxs(const float *xbl, const float *qwbl, uint8_t *y, const ota
                 sumqx += w * xval[i] * q;
                 sumq2 += w * q * q;
             }
-            OPS(32 * 7 + C_DIV * 2);
+            OPS(32 * 6 + C_DIV * 2);
             if (sumq2 > 0) scale = sumqx / sumq2;
         }
         if (scale < 0) {
@@ -501,7 +502,7 @@ static float iq2_16_search(const float *xb, const float *qw, float sigma2, int p
     }
     float mx = xval[0];
     for (int i = 1; i < 16; ++i) mx = GMAX(mx, xval[i]);
-    OPS(16);
+    OPS(16 + 16);
     memset(L, 0, sizeof L);
     gidx[0] = gidx[1] = -1;
     if (mx < eps) return 0.f;   /* the caller writes nothing for this sub-block */
@@ -520,7 +521,7 @@ static float iq2_16_search(const float *xb, const float *qw, float sigma2, int p
                 Laux[8 * k + i] = (int8_t)GMAX(0, GMIN(kMaxQ - 1, l));
                 u |= Laux[8 * k + i] << 2 * i;
             }
-            OPS(8 * 7 + 1);
+            OPS(8 * 5 + 1);
             const int m = map_at(t, u);
             on_grid_aux[k] = 1;
             if (m < 0) {
@@ -535,7 +536,7 @@ static float iq2_16_search(const float *xb, const float *qw, float sigma2, int p
             sumqx += w * xval[i] * q;
             sumq2 += w * q * q;
         }
-        OPS(16 * 7 + 5);
+        OPS(16 * 6 + 5);
         if (sumq2 > 0 && sumqx * sumqx > best * sumq2) {
             scale = sumqx / sumq2;
             best = scale * sumqx;
@@ -558,7 +559,7 @@ static float iq2_16_search(const float *xb, const float *qw, float sigma2, int p
                 u |= l << 2 * i;
                 L[8 * k + i] = (int8_t)l;
             }
-            OPS(8 * 7);
+            OPS(8 * 5);
             const int m = map_at(t, u);
             if (m < 0) nb_iq2(t, neigh_at(t, m), xval + 8 * k, waux + 8 * k, scale, L + 8 * k);
         }
@@ -569,7 +570,7 @@ static float iq2_16_search(const float *xb, const float *qw, float sigma2, int p
             sumqx += w * xval[i] * q;
             sumq2 += w * q * q;
         }
-        OPS(16 * 7 + C_DIV);
+        OPS(16 * 6 + C_DIV);
         if (sumq2 > 0) scale = sumqx / sumq2;
     }
     if (scale < 0) {
@@ -675,7 +676,7 @@ static void o_iq1_s(const float *xbl, const float *qwbl, uint8_t *y, const otab 
         iq_weights(qwbl + bs * ib, xb, sigma2, weight, bs);
         float mx = fabsf(xb[0]);
         for (int i = 1; i < bs; ++i) mx = GMAX(mx, fabsf(xb[i]));
-        OPS(2 * bs);
+        OPS(bs);
         if (mx < EPS_IQ1S) {
             scales[ib] = 0;
             shifts[ib] = 1;
@@ -697,22 +698,22 @@ static void o_iq1_s(const float *xbl, const float *qwbl, uint8_t *y, const otab 
                 float sumqx = (sumx[i1] - sumx[0]) * x_p[0] + (sumx[i2] - sumx[i1]) * x_p[1] + (sumx[bs] - sumx[i2]) * x_p[2];
                 float sumq2 = (sumw[i1] - sumw[0]) * x_p[0] * x_p[0] + (sumw[i2] - sumw[i1]) * x_p[1] * x_p[1] +
                               (sumw[bs] - sumw[i2]) * x_p[2] * x_p[2];
-                OPS(8 + 11 + 4);
+                OPS(17);
                 if (sumq2 > 0 && sumqx * sumqx > best_score * sumq2) {
                     scale = sumqx / sumq2;
                     best_score = scale * sumqx;
                     besti1 = i1; besti2 = i2; best_shift = 1;
-                    OPS(1 + C_DIV);
+                    OPS(5 + C_DIV);
                 }
                 sumqx = (sumx[i1] - sumx[0]) * x_m[0] + (sumx[i2] - sumx[i1]) * x_m[1] + (sumx[bs] - sumx[i2]) * x_m[2];
                 sumq2 = (sumw[i1] - sumw[0]) * x_m[0] * x_m[0] + (sumw[i2] - sumw[i1]) * x_m[1] * x_m[1] +
                         (sumw[bs] - sumw[i2]) * x_m[2] * x_m[2];
-                OPS(8 + 11 + 4);
+                OPS(17);
                 if (sumq2 > 0 && sumqx * sumqx > best_score * sumq2) {
                     scale = sumqx / sumq2;
                     best_score = scale * sumqx;
                     besti1 = i1; besti2 = i2; best_shift = -1;
-                    OPS(1 + C_DIV);
+                    OPS(5 + C_DIV);
                 }
             }
         }
@@ -752,7 +753,7 @@ static void o_iq1_s(const float *xbl, const float *qwbl, uint8_t *y, const otab 
                     sumq2 += w * q * q;
                 }
             }
-            OPS(bs * 6 + 2 + C_DIV);
+            OPS(bs * 7 + 2 + C_DIV);
             if (sumqx > 0 && sumq2 > 0) scale = sumqx / sumq2;
         }
         uint16_t h = 0;
@@ -800,7 +801,7 @@ static void o_iq1_m(const float *xbl, const float *qwbl, uint8_t *y, const otab 
         iq_weights(qwbl + bs * ib, xb, sigma2, weight, bs);
         float mx = fabsf(xb[0]);
         for (int i = 1; i < bs; ++i) mx = GMAX(mx, fabsf(xb[i]));
-        OPS(2 * bs);
+        OPS(bs);
         if (mx < EPS_IQ1M) {
             scales[ib] = 0;
             shifts[ib] = 0;
@@ -847,14 +848,14 @@ static void o_iq1_m(const float *xbl, const float *qwbl, uint8_t *y, const otab 
                 sumq2[1] = q2_p[0] + q2_m[1];
                 sumq2[2] = q2_m[0] + q2_p[1];
                 sumq2[3] = q2_m[0] + q2_m[1];
-                OPS(2 * 15 + 8);
+                OPS(26);
                 for (int k = 0; k < 4; ++k) {
-                    OPS(4);
+                    OPS(5);
                     if (sumq2[k] > 0 && sumqx[k] * sumqx[k] > best_score * sumq2[k]) {
                         scale = sumqx[k] / sumq2[k];
                         best_score = scale * sumqx[k];
                         besti1 = i1; besti2 = i2; best_k = k;
-                        OPS(1 + C_DIV);
+                        OPS(5 + C_DIV);
                     }
                 }
             }
@@ -896,7 +897,7 @@ static void o_iq1_m(const float *xbl, const float *qwbl, uint8_t *y, const otab 
                     sq2 += w * q * q;
                 }
             }
-            OPS(bs * 6 + 2 + C_DIV);
+            OPS(bs * 7 + 2 + C_DIV);
             if (sqx > 0 && sq2 > 0) scale = sqx / sq2;
         }
         qs[2 * ib + 0] = (uint8_t)(index[0] & 255);
@@ -918,7 +919,7 @@ static void o_iq1_m(const float *xbl, const float *qwbl, uint8_t *y, const otab 
         sc[ib / 4] |= (uint16_t)(l << 3 * (ib % 4));
         qh[ib] |= masks[shifts[ib]];
         const float *xb = xbl + bs * ib;
-        iq_weights(qwbl + bs * ib, xb, sigma2, weight, bs);
+        for (int i = 0; i < bs; ++i) weight[i] = qwbl[bs * ib + i] * sqrtf(sigma2 + xb[i] * xb[i]);   /* (same values as the first pass: not counted again) */
         for (int k = 0; k < 2; ++k) {
             const float *xx = k == 0 ? (shifts[ib] < 2 ? x_p : x_m) : (shifts[ib] % 2 == 0 ? x_p : x_m);
             const int8_t *pg = grid_pt(t, qs[2 * ib + k] + ((qh[ib] << (8 - 4 * k)) & 0x700));
@@ -929,7 +930,7 @@ static void o_iq1_m(const float *xbl, const float *qwbl, uint8_t *y, const otab 
                 sq2 += w * q * q;
             }
         }
-        OPS(6 + 16 * 7);
+        OPS(6 + 16 * 8);
     }
     if (sq2 > 0) d = sqx / sq2;
     const uint16_t s = f32_to_f16(d * 1.1125f);
@@ -962,7 +963,7 @@ static void o_iq3_xxs(const float *xbl, const float *qwbl, uint8_t *y, const ota
         for (int k = 0; k < 4; ++k) bsg[k] = signs_even(xb + 8 * k, weight + 8 * k, xval + 8 * k);
         float mx = xval[0];
         for (int i = 1; i < 32; ++i) mx = GMAX(mx, xval[i]);
-        OPS(32);
+        OPS(32 + 32);
         memset(L, 0, sizeof L);
         if (mx < EPS_IQ3XXS) {
             scales[ib] = 0;
@@ -983,7 +984,7 @@ static void o_iq3_xxs(const float *xbl, const float *qwbl, uint8_t *y, const ota
                     Laux[4 * k + i] = (int8_t)GMAX(0, GMIN(kMaxQ - 1, l));
                     u |= Laux[4 * k + i] << 3 * i;
                 }
-                OPS(4 * 7 + 1);
+                OPS(4 * 5 + 1);
                 const int m = map_at(t, u);
                 on_grid_aux[k] = 1;
                 if (m < 0) {
@@ -998,7 +999,7 @@ static void o_iq3_xxs(const float *xbl, const float *qwbl, uint8_t *y, const ota
                 sumqx += w * xval[i] * q;
                 sumq2 += w * q * q;
             }
-            OPS(32 * 7 + 5);
+            OPS(32 * 6 + 5);
             if (sumq2 > 0 && sumqx * sumqx > best * sumq2) {
                 scale = sumqx / sumq2;
                 best = scale * sumqx;
@@ -1020,7 +1021,7 @@ static void o_iq3_xxs(const float *xbl, const float *qwbl, uint8_t *y, const ota
                     l = GMAX(0, GMIN(kMaxQ - 1, l));
                     u |= l << 3 * i;
                 }
-                OPS(4 * 7);
+                OPS(4 * 5);
                 int gi = map_at(t, u);
                 if (gi < 0) gi = nb_iq3(t, neigh_at(t, gi), xval + 4 * k, waux + 4 * k, scale, L + 4 * k);
                 const int8_t *pg = grid_pt(t, gi);
@@ -1033,7 +1034,7 @@ static void o_iq3_xxs(const float *xbl, const float *qwbl, uint8_t *y, const ota
                 sumqx += w * xval[i] * q;
                 sumq2 += w * q * q;
             }
-            OPS(32 * 7 + C_DIV);
+            OPS(32 * 6 + C_DIV);
             if (sumq2 > 0) scale = sumqx / sumq2;
         }
         if (scale < 0) {
@@ -1119,7 +1120,7 @@ static void o_iq3_s(const float *xbl, const float *qwbl, uint8_t *y, const otab 
                     Laux[4 * k + i] = (int8_t)GMAX(0, GMIN(kMaxQ - 1, l));
                     u |= Laux[4 * k + i] << 3 * i;
                 }
-                OPS(4 * 7 + 1);
+                OPS(4 * 5 + 1);
                 const int m = map_at(t, u);
                 on_grid_aux[k] = 1;
                 if (m < 0) {
@@ -1134,7 +1135,7 @@ static void o_iq3_s(const float *xbl, const float *qwbl, uint8_t *y, const otab 
                 sumqx += w * xval[i] * q;
                 sumq2 += w * q * q;
             }
-            OPS(32 * 7 + 5);
+            OPS(32 * 6 + 5);
             if (sumq2 > 0 && sumqx * sumqx > best * sumq2) {
                 scale = sumqx / sumq2;
                 best = scale * sumqx;
@@ -1155,7 +1156,7 @@ static void o_iq3_s(const float *xbl, const float *qwbl, uint8_t *y, const otab 
                     l = GMAX(0, GMIN(kMaxQ - 1, l));
                     u |= l << 3 * i;
                 }
-                OPS(4 * 7);
+                OPS(4 * 5);
                 int gi = map_at(t, u);
                 if (gi < 0) gi = nb_iq3(t, neigh_at(t, gi), xval + 4 * k, waux + 4 * k, scale, L + 4 * k);
                 const int8_t *pg = grid_pt(t, gi);
@@ -1168,7 +1169,7 @@ static void o_iq3_s(const float *xbl, const float *qwbl, uint8_t *y, const otab 
                 sumqx += w * xval[i] * q;
                 sumq2 += w * q * q;
             }
-            OPS(32 * 7 + C_DIV);
+            OPS(32 * 6 + C_DIV);
             if (sumq2 > 0) scale = sumqx / sumq2;
         }
         if (scale < 0) {
@@ -1241,7 +1242,6 @@ static void iq4_impl(int SB, const float *x, uint8_t *dh, uint8_t *q4, uint16_t 
             iq_weights(qweights + ib * bsz, xb, sigma2, weight, bsz);
         } else {
             for (int j = 0; j < bsz; ++j) weight[j] = xb[j] * xb[j];
-            OPS(bsz);
         }
         float amax = 0, mx = 0;
         for (int j = 0; j < bsz; ++j) {
@@ -1359,7 +1359,7 @@ static float sym_levels(int n, int nmax, const float *x, int8_t *L, const float 
         sumlx += w * x[i] * l;
         suml2 += w * l * l;
     }
-    OPS(C_DIV + n * 12 + C_DIV + 2);
+    OPS(C_DIV + n * 10 + C_DIV + 2);
     float scale = suml2 ? sumlx / suml2 : 0.0f;
     float best = scale * sumlx;
     for (int is = -9; is <= 9; ++is) {
@@ -1372,12 +1372,12 @@ static float sym_levels(int n, int nmax, const float *x, int8_t *L, const float 
             sumlx += w * x[i] * l;
             suml2 += w * l * l;
         }
-        OPS(4 + C_DIV + n * 11 + 4);
+        OPS(3 + C_DIV + n * 9 + 5);
         if (suml2 > 0 && sumlx * sumlx > best * suml2) {
             for (int i = 0; i < n; ++i) L[i] = (int8_t)(nmax + GMAX(-nmax, GMIN(nmax - 1, near_int(iscale * x[i]))));
             scale = sumlx / suml2;
             best = scale * sumlx;
-            OPS(n * 6 + C_DIV + 1);
+            OPS(C_DIV + 1);
         }
     }
     return scale;
@@ -1446,7 +1446,7 @@ static float affine_levels(int with_im, int n, int nmax, const float *x, const f
         sum_w += w;
         sum_x += w * x[i];
     }
-    OPS(1 + n * 7 + 1);
+    OPS(1 + n * 5 + 1);
     if (mn > 0) mn = 0;
     if (with_im ? mx <= mn : mx == mn) {
         for (int i = 0; i < n; ++i) L[i] = 0;
@@ -1463,7 +1463,7 @@ static float affine_levels(int with_im, int n, int nmax, const float *x, const f
         const float w = with_im ? kw(weights, x, i) : weights[i];
         best += w * diff;
     }
-    OPS(2 + 2 * C_DIV + n * 13);
+    OPS(2 + 2 * C_DIV + n * 11);
     if (nstep < 1) {
         *the_min = -mn;
         return scale;
@@ -1486,7 +1486,7 @@ static float affine_levels(int with_im, int n, int nmax, const float *x, const f
             sum_xl += w * l * x[i];
         }
         const float D = sum_w * sum_l2 - sum_l * sum_l;
-        OPS(5 + C_DIV + n * 15 + 4);
+        OPS(5 + C_DIV + n * 13 + 4);
         if (!(D > 0)) continue;
         float this_scale = (sum_w * sum_xl - sum_x * sum_l) / D;
         float this_min = (sum_l2 * sum_x - sum_l * sum_xl) / D;
@@ -1546,7 +1546,7 @@ static void affine_final(const float *x, uint8_t *L, int g, int ng, int nmax, fl
         if (!dj) continue;
         const float mj = dmin * mn[j];
         for (int i = 0; i < g; ++i) L[g * j + i] = (uint8_t)GMAX(0, GMIN(nmax, near_int((x[g * j + i] + mj) / dj)));
-        OPS(2 + g * (1 + C_DIV + 2));
+        OPS(2 + g * (2 + C_DIV));
     }
 }
 
@@ -1649,7 +1649,7 @@ static void o_q3_k(const float *x, const float *qw, uint8_t *y) {
         OPS(2);
         if (!dj) continue;
         for (int i = 0; i < 16; ++i) L[16 * j + i] = (int8_t)(GMAX(-4, GMIN(3, near_int(x[16 * j + i] / dj))) + 4);
-        OPS(16 * (C_DIV + 4));
+        OPS(16 * (C_DIV + 2));
     }
     for (int j = 0; j < 32; ++j) hmask[j] = 0;
     for (int j = 0; j < QK; ++j)
@@ -1755,7 +1755,7 @@ static void o_q6_k(const float *x, const float *qw, uint8_t *y) {
         OPS(2);
         if (!dj) continue;
         for (int i = 0; i < 16; ++i) L[16 * j + i] = (int8_t)(GMAX(-32, GMIN(31, near_int(x[16 * j + i] / dj))) + 32);
-        OPS(16 * (C_DIV + 4));
+        OPS(16 * (C_DIV + 2));
     }
     for (int half = 0; half < 2; ++half) {
         const int8_t *Lh = L + 128 * half;
@@ -1776,7 +1776,7 @@ static void o_q8_0(const float *x, uint8_t *y) {
     const float id = d ? 1.0f / d : 0.0f;
     put16(y, f32_to_f16(d));
     for (int j = 0; j < 32; ++j) y[2 + j] = (uint8_t)(int8_t)roundf(x[j] * id);
-    OPS(2 * 32 + 2 * C_DIV + 1 + 32 * 3);
+    OPS(32 + 2 * C_DIV + 2 + 32 * 4);
 }
 
 /* ------------------------------------------------------------------ type traits and dispatch */
