@@ -1,0 +1,147 @@
+// trench-gguf_amd/csrc/coop.cuh - the wave-cooperative neighbour search of the i-quants.
+//
+// The reference scans a key's neighbour list serially on the thread that owns the key (gpuq/gpuq.hip:178-197,
+// 199-232, 971-992). Lists are 1 to ~190 points long, so a wave scanning its lanes' lists side by side runs as long
+// as its longest list while most lanes idle. Here the lists of the wave's 64 lanes are concatenated in lane order and
+// dealt out 64 candidates a round, one a lane, so every lane does useful work until the wave's total is exhausted.
+//
+// A candidate's distance is computed from the owner's values exactly as the serial scan computes it (same operands,
+// same operation order), and each owner's winner is the minimum of (distance bits, list position) over its
+// candidates, taken with LDS atomic mins. A distance is a sum of w*diff*diff terms from +0 with w >= 0 (or NaN
+// weights), so it is never negative and never -0: the unsigned order of its bits is the float order, with NaN above
+// +inf. The smallest position among equal distances is the serial scan's first-wins rule (it replaces only on a
+// strictly smaller distance), and a minimum at or above FLT_MAX is the serial scan accepting nothing (best starts at
+// FLT_MAX, strict <): the reference traps there, the caller flags it.
+//
+// The deal: lane L's list occupies positions [excl_L, incl_L) of the concatenation (a wave prefix sum). With
+// R = ceil(total / 64) rounds, lane L takes the contiguous run of positions [L*R, L*R + R): mostly one owner's
+// consecutive candidates, so the lane keeps that owner's values in registers, keeps a running minimum, and issues one
+// atomic min per owner it visits rather than one per candidate (many lanes of one owner hitting one LDS address in
+// the same instruction serialize). A lane finds the owner of its first position from a byte table the owners fill
+// (each owner marks the lanes whose first position falls in its range), then walks on to the next lane with a list
+// when the current owner's list ends.
+#pragma once
+#include "frame.cuh"
+
+// per-wave LDS workspace of the search
+struct CoopWS {
+    float stage[64][16];        // an owner's values: 8 (or 4) x's then 8 (or 4) weights
+    int4 info[64];              // owner: list offset, first position, scale bits, list length
+    unsigned long long key[64]; // owner: min of (distance bits << 32 | list position << 12 | grid index)
+    uint8_t mark[64];           // lane: the owner of its first position
+};
+static constexpr int COOP_WS_BYTES = (int)sizeof(CoopWS);
+
+// write this lane's values for the search: n values and n weights
+template <int NV> DEV void coop_stage(CoopWS &ws, const float *xv, const float *wv) {
+    float4 *s = (float4 *)ws.stage[lane_id()];
+#pragma unroll
+    for (int i = 0; i < NV / 4; ++i) {
+        s[i] = make_float4(xv[4 * i], xv[4 * i + 1], xv[4 * i + 2], xv[4 * i + 3]);
+        s[NV / 4 + i] = make_float4(wv[4 * i], wv[4 * i + 1], wv[4 * i + 2], wv[4 * i + 3]);
+    }
+}
+
+// inclusive prefix sum over the wave's 64 lanes (DPP: shifts within rows of 16, then the row broadcasts)
+DEV int wave_incl_scan(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);     // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);     // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);     // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);     // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);     // row_bcast:15 into rows 1 and 3
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);     // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
+// All 64 lanes call this together (wave-uniform control flow). cnt: the lane's list length (0: no search), off: the
+// list's offset in neigh (count at neigh[off], points from neigh[off + 1]), scale: the owner's scale. The lane's
+// values must have been staged (coop_stage) when cnt > 0.
+// Returns, for cnt > 0, the winning grid index (-1: no candidate accepted); for cnt == 0, -2.
+// ev(st, scale, idx): the distance of grid point idx (< 4096) for the owner's staged values st (16 floats).
+//
+// Rounds run in chunks of up to 8: the first pass walks the chunk's positions (owner, list position) and issues
+// their list reads, the second evaluates them, so a chunk's reads are in flight together. Positions past the end of
+// the concatenation repeat the lane's previous candidate, which leaves its running minimum unchanged.
+template <class Eval>
+DEV int coop_search(int cnt, int off, float scale, const uint16_t *neigh, CoopWS &ws, const Eval &ev) {
+    const int lane = lane_id();
+    const int incl = wave_incl_scan(cnt);
+    const int total = __builtin_amdgcn_readlane(incl, 63);
+    if (total == 0) return -2;                          // wave-uniform
+    const int excl = incl - cnt;
+    ws.info[lane] = make_int4(off, excl, __float_as_int(scale), cnt);
+    ws.key[lane] = ~0ull;
+    const int R = (total + 63) >> 6;                    // positions a lane
+    if (cnt > 0) {                                      // lanes L with excl <= L*R < incl start in this list
+        const int lf = (excl + R - 1) / R;
+        const int ll = (incl - 1) / R;
+        for (int L = lf; L <= ll && L < 64; ++L) ws.mark[L] = (uint8_t)lane;
+    }
+    wave_sync();
+    const unsigned long long has = __ballot(cnt > 0);
+    const int p0 = lane * R;
+    const int np = total - p0 < R ? (total - p0 > 0 ? total - p0 : 0) : R;   // this lane's positions
+    // walk state: owner, list position, the owner's list offset and length
+    int o = ws.mark[lane] & 63;
+    if (np == 0) o = 63 - __clzll(has);                 // (idle lane: any owner; it evaluates nothing new)
+    int4 oi = ws.info[o];
+    int j = np ? p0 - oi.y : 0;
+    j = j < 0 ? 0 : (j < oi.w ? j : oi.w - 1);          // (in range by construction; kept as a bound)
+    // evaluation state: the owner whose values are in registers, and the running minimum over its candidates
+    int cur = -1;
+    float st[16], sc = 0.f;
+    unsigned long long kmin = ~0ull;
+    for (int r0 = 0; r0 < R; r0 += 8) {
+        const int rend = R - r0 < 8 ? R - r0 : 8;
+        int own_j[8], idx[8];           // owner | list position << 6; the candidate's grid index
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            if (r < rend) {
+                if (r0 + r < np) {
+                    if (j >= oi.w) {                    // the owner's list ends: on to the next lane with a list
+                        const unsigned long long nx = has & ~((2ull << o) - 1);
+                        o = nx ? __ffsll((long long)nx) - 1 : o;
+                        oi = ws.info[o];
+                        j = 0;
+                    }
+                    const int jc = j < oi.w ? j : oi.w - 1;   // (always j: kept as a bound)
+                    own_j[r] = o | (jc << 6);
+                    idx[r] = neigh[oi.x + 1 + jc];
+                    ++j;
+                } else {                                // past this lane's positions: repeat the last candidate
+                    own_j[r] = r ? own_j[r - 1] : -1;
+                    idx[r] = r ? idx[r - 1] : 0;
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            if (r < rend) {
+                const int owner = own_j[r] & 63;
+                const bool valid = own_j[r] >= 0;
+                if (valid && owner != cur) {
+                    if (cur >= 0) atomicMin(&ws.key[cur], kmin);
+                    cur = owner;
+                    kmin = ~0ull;
+                    const float4 *sp = (const float4 *)ws.stage[owner];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float4 v = sp[i];
+                        st[4 * i] = v.x; st[4 * i + 1] = v.y; st[4 * i + 2] = v.z; st[4 * i + 3] = v.w;
+                    }
+                    sc = __int_as_float(ws.info[owner].z);
+                }
+                const float d2 = ev(st, sc, idx[r]);
+                const unsigned long long key = ((unsigned long long)__float_as_uint(d2) << 32) |
+                                               (((unsigned)(own_j[r] >> 6) << 12) | (unsigned)idx[r]);
+                if (valid && key < kmin) kmin = key;
+            }
+        }
+    }
+    if (cur >= 0) atomicMin(&ws.key[cur], kmin);
+    wave_sync();
+    if (cnt <= 0) return -2;
+    const unsigned long long k = ws.key[lane];
+    if ((unsigned)(k >> 32) >= 0x7f7fffffu) return -1;  // min distance >= FLT_MAX (or NaN): nothing accepted
+    return (int)(k & 0xfffu);
+}

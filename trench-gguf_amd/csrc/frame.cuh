@@ -21,7 +21,8 @@ struct QParams {
     uint8_t *dst;           // output blocks
     int64_t nsb;            // units: super-blocks, or 32-blocks for Q8_0 / IQ4_NL
     // i-quant tables (device): search grid, full 2-bit / 3-bit key map, ggml-layout neighbour lists, and for the
-    // 8-value types the map re-indexed by base-3 keys (levels 0..2), staged into LDS by the kernels
+    // 8-value types the map re-indexed by base-3 keys (levels 0..2, off-grid entries packed as below), staged into
+    // LDS by the kernels
     const uint64_t *grid;
     const int32_t *map;
     const uint16_t *neigh;
@@ -33,6 +34,11 @@ struct QParams {
     // b*out_stride + out_off. The contiguous defaults are sb_stride = BS, qw_stride = BS, out_stride = BB, 0 offsets.
     int64_t sb_stride, sb_off, qw_stride, qw_off, out_stride, out_off;
 };
+
+// map3 entries: >= 0 a grid index; < 0 an off-grid key, -1 - (list offset | list length << M3_OFF_BITS)
+#define M3_OFF_BITS 21
+DEV int m3_off(int m) { return (-m - 1) & ((1 << M3_OFF_BITS) - 1); }
+DEV int m3_cnt(int m) { return (-m - 1) >> M3_OFF_BITS; }
 
 DEV int64_t qw_row(const QParams &p, int64_t b) { return (b / p.qw_mat) * p.qw_mod + (b % p.qw_mod) / p.qw_div; }
 
@@ -92,10 +98,18 @@ DEV void img_store(uint8_t *dst, const uint8_t *img, int nbytes) {
 // TAB (LDS table bytes, 0 for none),
 // stage(p, lds) (cooperative table staging, before the barrier), and
 // quant(x, qw, g, img, boff, lds, p): lane g's part of one super-block, OR-ing its bytes into img at boff.
+// WS (optional, bytes, multiple of 16): a per-wave LDS workspace placed right after the wave's image
 template <class T> constexpr int img_bytes() { return ((64 / T::G) * T::BB + 15) & ~15; }
+template <class T, class = void> struct ws_of { static constexpr int v = 0; };
+template <class T> struct ws_of<T, decltype((void)T::WS)> { static constexpr int v = T::WS; };
+template <class T> constexpr int wave_bytes() { return img_bytes<T>() + ws_of<T>::v; }
+template <class T> DEV uint8_t *wave_ws(uint8_t *img) { return img + img_bytes<T>(); }
+// WPE (optional): the waves per SIMD the register allocation must allow (default 2)
+template <class T, class = void> struct wpe_of { static constexpr int v = 2; };
+template <class T> struct wpe_of<T, decltype((void)T::WPE)> { static constexpr int v = T::WPE; };
 
 template <class T, int SRC>
-__global__ __launch_bounds__(WG_THREADS) void k_quant(QParams p) {
+__global__ __launch_bounds__(WG_THREADS) __attribute__((amdgpu_waves_per_eu(wpe_of<T>::v))) void k_quant(QParams p) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int SPW = 64 / T::G;
     if (T::TAB) {
@@ -104,7 +118,7 @@ __global__ __launch_bounds__(WG_THREADS) void k_quant(QParams p) {
     }
     const int wave = (int)(threadIdx.x >> 6), lane = lane_id();
     const int g = lane % T::G, slot = lane / T::G;
-    uint8_t *img = lds + T::TAB + wave * img_bytes<T>();
+    uint8_t *img = lds + T::TAB + wave * wave_bytes<T>();
     const int64_t nwaves = (int64_t)gridDim.x * WG_WAVES;
     for (int64_t t = (int64_t)blockIdx.x * WG_WAVES + wave; t * SPW < p.nsb; t += nwaves) {
         const int64_t b0 = t * SPW;

@@ -111,6 +111,7 @@ bool valid_search(int t, const std::vector<uint64_t> &grid, const std::vector<in
         if (off >= NL) return false;
         const int cnt = neigh[off];
         if (cnt < 1 || off + cnt >= NL) return false;
+        if (e8 && (off >= (1 << M3_OFF_BITS) || cnt >= (1 << (31 - M3_OFF_BITS)))) return false;
         for (int j = 1; j <= cnt; ++j)
             if (neigh[off + j] >= G) return false;
     }
@@ -131,7 +132,7 @@ template <class T, int SRC> bool launch_q(const QParams &p, hipStream_t st) {
     const int64_t cap = (int64_t)g_ncu * 8;
     if (wgs > cap) wgs = cap;
     if (wgs < 1) wgs = 1;
-    const size_t lds = (size_t)T::TAB + WG_WAVES * img_bytes<T>();
+    const size_t lds = (size_t)T::TAB + WG_WAVES * wave_bytes<T>();
     hipLaunchKernelGGL((k_quant<T, SRC>), dim3((unsigned)wgs), dim3(WG_THREADS), lds, st, p);
     return hipGetLastError() == hipSuccess;
 }
@@ -364,7 +365,9 @@ extern "C" int gpuq_init(const char *tables, int device) {
                 for (int k = 0; k < 6561; ++k) {
                     int u = 0, rr = k;
                     for (int i = 0; i < 8; ++i) { u |= (rr % 3) << (2 * i); rr /= 3; }
-                    m3[k] = r.map[u];
+                    const int m = r.map[u];
+                    // off-grid: the list offset and its length packed (m3_off / m3_cnt), checked by valid_search
+                    m3[k] = m >= 0 ? m : -1 - ((-m - 1) | ((int)r.neigh[-(int64_t)m - 1] << M3_OFF_BITS));
                 }
                 if (!upload(&t.map3, m3)) return 4;
             }

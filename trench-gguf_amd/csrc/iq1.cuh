@@ -163,7 +163,7 @@ struct KIQ1S : Iq8Tab<2048> {
                     int gi = m;
                     if (m < 0) {
                         all_on_grid = false;
-                        gi = nb_best_iq1(p.neigh + (-m - 1), grid, x + 8 * k, weight + 8 * k, scale, minus);
+                        gi = nb_best_iq1(p.neigh + m3_off(m), grid, x + 8 * k, weight + 8 * k, scale, minus);
                         if (gi < 0) { flag_err(p); gi = 0; }
                     }
                     gi4[k] = gi;
@@ -316,7 +316,7 @@ struct KIQ1M : Iq8Tab<2048> {
                     int gi = m;
                     if (m < 0) {
                         all_on_grid = false;
-                        gi = nb_best_iq1(p.neigh + (-m - 1), grid, x + 8 * k, weight + 8 * k, scale, minus);
+                        gi = nb_best_iq1(p.neigh + m3_off(m), grid, x + 8 * k, weight + 8 * k, scale, minus);
                         if (gi < 0) { flag_err(p); gi = 0; }
                     }
                     gi2[k] = gi;

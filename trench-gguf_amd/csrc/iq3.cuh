@@ -10,6 +10,20 @@
 #define EPS_IQ3XXS 1e-8f
 #define NKEY8 4096
 
+// sum over the sub-block of w*x*q and w*q*q with q = 2l+1 from the packed point bytes (index order)
+template <int N> DEV void sums_q(const float (&weight)[N], const float (&xval)[N], const uint32_t (&P)[N / 4],
+                                 float &sumqx, float &sumq2) {
+    sumqx = 0;
+    sumq2 = 0;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const float w = weight[i];
+        const float q = (float)((P[i / 4] >> (8 * (i % 4))) & 0xffu);
+        sumqx += w * xval[i] * q;
+        sumq2 += w * q * q;
+    }
+}
+
 template <int GRID> struct Iq4Tab {
     static constexpr int GRIDB = GRID * 4;
     static constexpr int TAB = (GRIDB + NKEY8 * 4 + 15) & ~15;
