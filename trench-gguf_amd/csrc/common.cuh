@@ -24,6 +24,8 @@ DEV float fmax_sel(float a, float b) { return a > b ? a : b; }   // ggml's MAX m
 DEV float fmin_sel(float a, float b) { return a < b ? a : b; }
 DEV int imax(int a, int b) { return a > b ? a : b; }
 DEV int imin(int a, int b) { return a < b ? a : b; }
+// make v opaque to the optimizer at this point (no instruction): expressions of v are not hoisted across it
+DEV void opaque(float &v) { asm volatile("" : "+v"(v)); }
 
 // RNE fp32 -> fp16 through the fp32 adder; NaN -> 0x7E00
 DEV uint16_t f2h(float f) {

@@ -26,7 +26,7 @@
 // per-wave LDS workspace of the search
 struct CoopWS {
     float stage[64][16];        // an owner's values: 8 (or 4) x's then 8 (or 4) weights
-    int4 info[64];              // owner: list offset, first position, scale bits, list length
+    int4 info[64];              // owner: list offset, first position, scale bits, list length | next owner << 16
     unsigned long long key[64]; // owner: min of (distance bits << 32 | list position << 12 | grid index)
     uint8_t mark[64];           // lane: the owner of its first position
 };
@@ -40,6 +40,14 @@ template <int NV> DEV void coop_stage(CoopWS &ws, const float *xv, const float *
         s[i] = make_float4(xv[4 * i], xv[4 * i + 1], xv[4 * i + 2], xv[4 * i + 3]);
         s[NV / 4 + i] = make_float4(wv[4 * i], wv[4 * i + 1], wv[4 * i + 2], wv[4 * i + 3]);
     }
+}
+
+// a / b for 0 <= a < 2^20, 1 <= b < 2^12: a float quotient, corrected to the floor
+DEV int div_small(int a, int b) {
+    int q = (int)((float)a * (1.0f / (float)b));
+    q += (q + 1) * b <= a;
+    q -= q * b > a;
+    return q;
 }
 
 // inclusive prefix sum over the wave's 64 lanes (DPP: shifts within rows of 16, then the row broadcasts)
@@ -57,11 +65,11 @@ DEV int wave_incl_scan(int v) {
 // list's offset in neigh (count at neigh[off], points from neigh[off + 1]), scale: the owner's scale. The lane's
 // values must have been staged (coop_stage) when cnt > 0.
 // Returns, for cnt > 0, the winning grid index (-1: no candidate accepted); for cnt == 0, -2.
-// ev(st, scale, idx): the distance of grid point idx (< 4096) for the owner's staged values st (16 floats).
+// ev.point(idx): grid point idx (< 4096) as stored; ev(st, scale, pt): its distance for the owner's staged values st
+// (16 floats).
 //
-// Rounds run in chunks of up to 8: the first pass walks the chunk's positions (owner, list position) and issues
-// their list reads, the second evaluates them, so a chunk's reads are in flight together. Positions past the end of
-// the concatenation repeat the lane's previous candidate, which leaves its running minimum unchanged.
+// Rounds run in chunks of up to 8: a first pass walks the chunk's positions (owner, list position) and issues their
+// list reads, a second reads their grid points, a third evaluates them, so a chunk's reads are in flight together.
 template <class Eval>
 DEV int coop_search(int cnt, int off, float scale, const uint16_t *neigh, CoopWS &ws, const Eval &ev) {
     const int lane = lane_id();
@@ -69,24 +77,28 @@ DEV int coop_search(int cnt, int off, float scale, const uint16_t *neigh, CoopWS
     const int total = __builtin_amdgcn_readlane(incl, 63);
     if (total == 0) return -2;                          // wave-uniform
     const int excl = incl - cnt;
-    ws.info[lane] = make_int4(off, excl, __float_as_int(scale), cnt);
+    const unsigned long long has = __ballot(cnt > 0);
+    const unsigned long long after = has & ~((2ull << lane) - 1);
+    const int next = after ? __ffsll((long long)after) - 1 : lane;     // the next lane with a list
+    ws.info[lane] = make_int4(off, excl, __float_as_int(scale), cnt | (next << 16));
     ws.key[lane] = ~0ull;
     const int R = (total + 63) >> 6;                    // positions a lane
     if (cnt > 0) {                                      // lanes L with excl <= L*R < incl start in this list
-        const int lf = (excl + R - 1) / R;
-        const int ll = (incl - 1) / R;
+        const int lf = div_small(excl + R - 1, R);
+        const int ll = div_small(incl - 1, R);
         for (int L = lf; L <= ll && L < 64; ++L) ws.mark[L] = (uint8_t)lane;
     }
     wave_sync();
-    const unsigned long long has = __ballot(cnt > 0);
     const int p0 = lane * R;
     const int np = total - p0 < R ? (total - p0 > 0 ? total - p0 : 0) : R;   // this lane's positions
-    // walk state: owner, list position, the owner's list offset and length
+    // walk state: owner, list position, the owner's list length and its first entry
     int o = ws.mark[lane] & 63;
-    if (np == 0) o = 63 - __clzll(has);                 // (idle lane: any owner; it evaluates nothing new)
+    if (np == 0) o = 63 - __clzll(has);                 // (idle lane: repeats the last owner's candidates)
     int4 oi = ws.info[o];
+    int ocnt = oi.w & 0xffff;
+    const uint16_t *ol = neigh + oi.x + 1;
     int j = np ? p0 - oi.y : 0;
-    j = j < 0 ? 0 : (j < oi.w ? j : oi.w - 1);          // (in range by construction; kept as a bound)
+    int4 ni = ws.info[oi.w >> 16];                      // the next owner's entry, read ahead of its use
     // evaluation state: the owner whose values are in registers, and the running minimum over its candidates
     int cur = -1;
     float st[16], sc = 0.f;
@@ -94,32 +106,34 @@ DEV int coop_search(int cnt, int off, float scale, const uint16_t *neigh, CoopWS
     for (int r0 = 0; r0 < R; r0 += 8) {
         const int rend = R - r0 < 8 ? R - r0 : 8;
         int own_j[8], idx[8];           // owner | list position << 6; the candidate's grid index
+        uint64_t pt[8];                 // the candidate's grid point
+        // walk: past this lane's positions the walk stays in the owner it is in (list position clamped), so every
+        // slot holds a valid candidate of that owner and repeats change no minimum
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
             if (r < rend) {
-                if (r0 + r < np) {
-                    if (j >= oi.w) {                    // the owner's list ends: on to the next lane with a list
-                        const unsigned long long nx = has & ~((2ull << o) - 1);
-                        o = nx ? __ffsll((long long)nx) - 1 : o;
-                        oi = ws.info[o];
-                        j = 0;
-                    }
-                    const int jc = j < oi.w ? j : oi.w - 1;   // (always j: kept as a bound)
-                    own_j[r] = o | (jc << 6);
-                    idx[r] = neigh[oi.x + 1 + jc];
-                    ++j;
-                } else {                                // past this lane's positions: repeat the last candidate
-                    own_j[r] = r ? own_j[r - 1] : -1;
-                    idx[r] = r ? idx[r - 1] : 0;
+                if (j >= ocnt && r0 + r < np) {         // the owner's list ends: on to the next lane with a list
+                    o = oi.w >> 16;
+                    oi = ni;
+                    ocnt = oi.w & 0xffff;
+                    ol = neigh + oi.x + 1;
+                    j = 0;
+                    ni = ws.info[oi.w >> 16];           // (not needed before the next change of owner)
                 }
+                const int jc = j < ocnt ? j : ocnt - 1;
+                own_j[r] = o | (jc << 6);
+                idx[r] = ol[jc];
+                ++j;
             }
         }
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+            if (r < rend) pt[r] = ev.point(idx[r]);
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
             if (r < rend) {
                 const int owner = own_j[r] & 63;
-                const bool valid = own_j[r] >= 0;
-                if (valid && owner != cur) {
+                if (owner != cur) {
                     if (cur >= 0) atomicMin(&ws.key[cur], kmin);
                     cur = owner;
                     kmin = ~0ull;
@@ -131,10 +145,10 @@ DEV int coop_search(int cnt, int off, float scale, const uint16_t *neigh, CoopWS
                     }
                     sc = __int_as_float(ws.info[owner].z);
                 }
-                const float d2 = ev(st, sc, idx[r]);
+                const float d2 = ev(st, sc, pt[r]);
                 const unsigned long long key = ((unsigned long long)__float_as_uint(d2) << 32) |
                                                (((unsigned)(own_j[r] >> 6) << 12) | (unsigned)idx[r]);
-                if (valid && key < kmin) kmin = key;
+                kmin = key < kmin ? key : kmin;
             }
         }
     }

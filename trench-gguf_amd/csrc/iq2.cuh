@@ -54,8 +54,8 @@ DEV void flag_err(const QParams &p) { atomicOr(p.err, 1); }
 // (st[0..7] the x's, st[8..15] the weights), in the serial scan's operation order
 struct EvalIq8 {
     const uint64_t *grid;
-    DEV float operator()(const float *st, float scale, int idx) const {
-        const uint64_t pt = grid[idx];
+    DEV uint64_t point(int idx) const { return grid[idx]; }
+    DEV float operator()(const float *st, float scale, uint64_t pt) const {
         const uint32_t lo = (uint32_t)pt, hi = (uint32_t)(pt >> 32);
         float d2 = 0;
 #pragma unroll
@@ -69,16 +69,16 @@ struct EvalIq8 {
 };
 
 // The group's grid point on every lane of the wave (all lanes call it together): an active lane whose key is on the
-// grid takes that point (og = true), the others search their neighbour lists together (coop_search). Inactive lanes
-// get 0. A search that accepts nothing flags the error (the reference traps) and yields 0.
-DEV int group_point_w(bool active, int k3, const int32_t *map3, const QParams &p, const uint64_t *grid,
-                      const float *xv, const float *wa, float scale, CoopWS &ws, bool &og) {
+// grid takes that point (og = true), the others search their neighbour lists together (coop_search) with the values
+// the caller staged (coop_stage). Inactive lanes get 0. A search that accepts nothing flags the error (the reference
+// traps) and yields 0.
+DEV int group_point_s(bool active, int k3, const int32_t *map3, const QParams &p, const uint64_t *grid, float scale,
+                      CoopWS &ws, bool &og) {
     const int m = active ? map3[k3] : 0;
     og = m >= 0;
     const bool srch = active && m < 0;
     const int off = srch ? m3_off(m) : 0;
     const int cnt = srch ? m3_cnt(m) : 0;
-    if (srch) coop_stage<8>(ws, xv, wa);
     const int gi = coop_search(cnt, off, scale, p.neigh, ws, EvalIq8{grid});
     if (!srch) return active ? m : 0;
     if (gi < 0) {
@@ -86,6 +86,13 @@ DEV int group_point_w(bool active, int k3, const int32_t *map3, const QParams &p
         return 0;
     }
     return gi;
+}
+
+// the same, staging the group's values (x's xv, weights wa) first
+DEV int group_point_w(bool active, int k3, const int32_t *map3, const QParams &p, const uint64_t *grid,
+                      const float *xv, const float *wa, float scale, CoopWS &ws, bool &og) {
+    coop_stage<8>(ws, xv, wa);
+    return group_point_s(active, k3, map3, p, grid, scale, ws, og);
 }
 
 // signs of 8 values with even parity: an odd count flips the weight with the least w*x^2 (gpuq/gpuq.hip:272-289)
@@ -122,6 +129,18 @@ DEV uint32_t signs_plain8(const float *xb, float *xval) {
     return s;
 }
 
+// rotate a sub-block's 32 values left by one group (four rotations restore the order): a rolled loop over the
+// groups then always finds the current group at [0, 8) and never indexes registers with a variable
+DEV void rot8(float (&v)[32]) {
+    float t[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) t[i] = v[i];
+#pragma unroll
+    for (int i = 0; i < 24; ++i) v[i] = v[i + 8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[24 + i] = t[i];
+}
+
 // one group's terms of the sub-block sums of w*x*q and w*q*q (q = 2l+1 from the point's bytes), added in index order
 DEV void sums_q8(const float *w, const float *xv, uint64_t pt, float &sumqx, float &sumq2) {
     const uint32_t lo = (uint32_t)pt, hi = (uint32_t)(pt >> 32);
@@ -136,12 +155,15 @@ DEV void sums_q8(const float *w, const float *xv, uint64_t pt, float &sumqx, flo
 // ------------------------------------------------------------------ IQ2_XXS (gpuq/gpuq.hip:245-387)
 // block: d qs[32] u16 (66 bytes); lane g = 32-weight sub-block g; q2[2g] at 2+8g, q2[2g+1] at 6+8g
 struct KIQ2XXS : Iq8Tab<256> {
-    static constexpr int BS = QK, G = 8, N = 32, BB = 66, WS = COOP_WS_BYTES;
+    static constexpr int BS = QK, G = 8, N = 32, BB = 66, NTRIAL = 13;
+    // per-wave LDS: the search workspace, then every trial's 4 grid indices (a u32 per trial and lane)
+    static constexpr int WS = COOP_WS_BYTES + NTRIAL * 64 * 4;
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
                           const QParams &p) {
         const uint64_t *grid = Iq8Tab<256>::grid(lds);
         const int32_t *map3 = Iq8Tab<256>::map3(lds);
         CoopWS &ws = *(CoopWS *)wave_ws<KIQ2XXS>(img);
+        uint32_t *gtab = (uint32_t *)(wave_ws<KIQ2XXS>(img) + COOP_WS_BYTES) + lane_id();   // [trial * 64]
         float weight[N], xval[N];
         uint32_t bsg = 0;       // the 4 groups' 7-bit sign fields
         {
@@ -167,26 +189,36 @@ struct KIQ2XXS : Iq8Tab<256> {
             if (eff_max <= 0) scale = 0.f;
             else live = true;
         }
-        float waux[N];
+        // The trials' groups, group by group (every lane runs them: the neighbour search is wave-wide): a group's
+        // values are staged once for its 13 trial scales, and trial t's grid index of group k goes to byte k of
+        // gtab[t]. Each trial's searches do not depend on another trial's outcome, so the order changes nothing.
+#pragma unroll 1
+        for (int k = 0; k < 4; ++k) {           // (not unrolled: one copy of the search code, groups kept apart)
+            const float *xk = xval;            // group k: rotated to the front (rot8 below)
+            float waux[8];
 #pragma unroll
-        for (int i = 0; i < N; ++i) waux[i] = sqrtf(weight[i]);
-        // the trial scales: every lane runs them (the neighbour search is wave-wide); only live lanes use them
+            for (int i = 0; i < 8; ++i) waux[i] = sqrtf(weight[i]);
+            coop_stage<8>(ws, xk, waux);
+#pragma unroll 1
+            for (int t = 0; t < NTRIAL; ++t) {
+                const float id = (5 + (t - 6) * 0.1f) / eff_max;
+                const float this_scale = 1 / id;
+                bool og;
+                const int gi = group_point_s(live, group_key3(xk, id), map3, p, grid, this_scale, ws, og);
+                ((uint8_t *)(gtab + t * 64))[k] = (uint8_t)gi;
+            }
+            rot8(xval);
+            rot8(weight);
+        }
+        // the acceptance chain over the trials, in ggml's order
         float best = 0;
         uint32_t P = 0;         // accepted trial's groups: grid indices, a byte each
 #pragma unroll 1
-        for (int is = -6; is <= 6; ++is) {
-            const float id = (5 + is * 0.1f) / eff_max;
-            const float this_scale = 1 / id;
-            uint32_t Pa = 0;
+        for (int t = 0; t < NTRIAL; ++t) {
+            const uint32_t Pa = gtab[t * 64];
             float sumqx = 0, sumq2 = 0;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                bool og;
-                const int gi = group_point_w(live, group_key3(xval + 8 * k, id), map3, p, grid, xval + 8 * k,
-                                             waux + 8 * k, this_scale, ws, og);
-                Pa |= (uint32_t)gi << (8 * k);
-                sums_q8(weight + 8 * k, xval + 8 * k, grid[gi], sumqx, sumq2);
-            }
+            for (int k = 0; k < 4; ++k) sums_q8(weight + 8 * k, xval + 8 * k, grid[(Pa >> (8 * k)) & 255], sumqx, sumq2);
             if (live && sumq2 > 0 && sumqx * sumqx > best * sumq2) {
                 scale = sumqx / sumq2;
                 best = scale * sumqx;
@@ -199,13 +231,17 @@ struct KIQ2XXS : Iq8Tab<256> {
             const float id = 1 / scale;
             uint32_t Pf = 0;
             float sumqx = 0, sumq2 = 0;
-#pragma unroll
+#pragma unroll 1
             for (int k = 0; k < 4; ++k) {
+                float waux[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) waux[i] = sqrtf(weight[i]);
                 bool og;
-                const int gi = group_point_w(fin, group_key3(xval + 8 * k, id), map3, p, grid, xval + 8 * k,
-                                             waux + 8 * k, scale, ws, og);
+                const int gi = group_point_w(fin, group_key3(xval, id), map3, p, grid, xval, waux, scale, ws, og);
                 Pf |= (uint32_t)gi << (8 * k);
-                sums_q8(weight + 8 * k, xval + 8 * k, grid[gi], sumqx, sumq2);
+                sums_q8(weight, xval, grid[gi], sumqx, sumq2);
+                rot8(xval);
+                rot8(weight);
             }
             if (fin) {
                 P = Pf;
