@@ -8,6 +8,7 @@
 //    acceptance chain is ggml's exactly. Its loop indices are wave-uniform, so the prefix arrays are indexed through
 //    uniform (M0-relative) register addressing.
 //  - IQ1_M's final least-squares d over all 256 weights is a lane-to-lane chain in ggml's index order.
+//  - The neighbour searches of the final points run wave-wide (coop.cuh), so every lane takes part in them.
 // Tables: the 2048-point IQ1 grid and its base-3 key map in LDS (the IQ1 levels are always 0..2), lists in HBM.
 #pragma once
 #include "iq2.cuh"
@@ -24,26 +25,44 @@ DEV float iq1_val(int l, bool minus) {
     return l == 0 ? a : (l == 1 ? b : c);
 }
 
-// iq1_find_best_neighbour2 over a list (gpuq/gpuq.hip:199-232); -1 when no neighbour has a finite distance (the
-// reference then scans the whole grid with an out-of-block read; that case is reported as an error here)
-DEV int nb_best_iq1(const uint16_t *nb, const uint64_t *grid, const float *xv, const float *w, float scale,
-                    bool minus) {
-    const int cnt = nb[0];
-    float best = FLT_MAX;
-    int gi = -1;
-    for (int j = 1; j <= cnt; ++j) {
-        const int idx = nb[j];
-        const uint64_t pt = grid[idx];
+// iq1_find_best_neighbour2's distance of one grid point (gpuq/gpuq.hip:199-232) for an owner's staged values
+// (st[0..7] the x's, st[8..15] the weights), in the serial scan's operation order. The owner's shift rides on the
+// sign of its (positive) scale; a level's value (l - 1) +- 1/8 = b/2 - 3/2 +- 1/8 from the point byte b = 2l + 1 is
+// exact in float, so it equals ggml's table entry. (A key with no finite distance makes the reference scan the whole
+// grid with an out-of-block read; the caller reports it as an error.)
+struct EvalIq1 {
+    const uint64_t *grid;
+    DEV uint64_t point(int idx) const { return grid[idx]; }
+    DEV float operator()(const float *st, float ssc, uint64_t pt) const {
+        const float scale = fabsf(ssc);
+        const float c = ssc < 0 ? -1.5f - IQ1_DELTA : -1.5f + IQ1_DELTA;
         const uint32_t lo = (uint32_t)pt, hi = (uint32_t)(pt >> 32);
         float d2 = 0;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const int b = (int)(((i < 4 ? lo : hi) >> (8 * (i % 4))) & 0xffu);
-            const float q = iq1_val((b - 1) / 2, minus);
-            const float diff = scale * q - xv[i];
-            d2 += w[i] * diff * diff;
+            const float q = (float)(((i < 4 ? lo : hi) >> (8 * (i % 4))) & 0xffu) * 0.5f + c;
+            const float diff = scale * q - st[i];
+            d2 += st[8 + i] * diff * diff;
         }
-        if (d2 < best) { best = d2; gi = idx; }
+        return d2;
+    }
+};
+
+// Group k's grid point on every lane of the wave (all lanes call it together; k, live as the caller has them): a key
+// on the grid directly, else the cooperative search over its list. Returns 0 for a lane that is not live, and flags
+// a search that accepts nothing.
+DEV int iq1_group_point(bool live, int m, const float *xk, const float *wk, float scale, bool minus,
+                        const QParams &p, const uint64_t *grid, CoopWS &ws, bool &on_grid) {
+    const bool srch = live && m < 0;
+    on_grid = !srch;
+    const int cnt = srch ? m3_cnt(m) : 0, off = srch ? m3_off(m) : 0;
+    if (srch) coop_stage<8>(ws, xk, wk);
+    const int gi = coop_search(cnt, off, minus ? -scale : scale, p.neigh, ws, EvalIq1{grid});
+    if (!live) return 0;
+    if (!srch) return m;
+    if (gi < 0) {
+        flag_err(p);
+        return 0;
     }
     return gi;
 }
@@ -82,7 +101,7 @@ template <int G, int N> DEV void grp_chain_sum2(const float (&a)[N], const float
 // ------------------------------------------------------------------ IQ1_S (gpuq/gpuq.hip:389-514)
 // block: d qs[32] qh[8] u16 (50 bytes); lane g = 32-weight block g
 struct KIQ1S : Iq8Tab<2048> {
-    static constexpr int BS = QK, G = 8, N = 32, BB = 50;
+    static constexpr int BS = QK, G = 8, N = 32, BB = 50, WS = COOP_WS_BYTES;
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
                           const QParams &p) {
         const uint64_t *grid = Iq8Tab<2048>::grid(lds);
@@ -101,7 +120,8 @@ struct KIQ1S : Iq8Tab<2048> {
         for (int i = 1; i < N; ++i) mx = fmax_sel(mx, fabsf(x[i]));
         bool live = false, minus = false;
         float scale = 0.f;
-        int gi4[4] = {0, 0, 0, 0};
+        int gi4[4] = {0, 0, 0, 0}, m4[4] = {0, 0, 0, 0};
+        CoopWS &ws = *(CoopWS *)wave_ws<KIQ1S>(img);
         if (!(mx < EPS_IQ1S)) {
             Lv<N> R;
             stable_ranks<N>(x, R);
@@ -147,7 +167,6 @@ struct KIQ1S : Iq8Tab<2048> {
                 const bool flip = scale < 0;
                 if (flip) { scale = -scale; best_shift = -best_shift; }
                 minus = best_shift != 1;
-                bool all_on_grid = true;
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     int k3 = 0, p3 = 1;
@@ -159,15 +178,20 @@ struct KIQ1S : Iq8Tab<2048> {
                         k3 += l * p3;
                         p3 *= 3;
                     }
-                    const int m = map3[k3];
-                    int gi = m;
-                    if (m < 0) {
-                        all_on_grid = false;
-                        gi = nb_best_iq1(p.neigh + m3_off(m), grid, x + 8 * k, weight + 8 * k, scale, minus);
-                        if (gi < 0) { flag_err(p); gi = 0; }
-                    }
-                    gi4[k] = gi;
+                    m4[k] = map3[k3];
                 }
+            }
+        }
+        // the groups' points (every lane: the neighbour search is wave-wide)
+        bool all_on_grid = true;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            bool og;
+            gi4[k] = iq1_group_point(live, m4[k], x + 8 * k, weight + 8 * k, scale, minus, p, grid, ws, og);
+            all_on_grid = all_on_grid && og;
+        }
+        if (live) {
+            {
                 if (!all_on_grid) {
                     float sumqx = 0, sumq2 = 0;
 #pragma unroll
@@ -209,7 +233,7 @@ struct KIQ1S : Iq8Tab<2048> {
 // ------------------------------------------------------------------ IQ1_M (gpuq/gpuq.hip:516-688)
 // block: qs[32] qh[16] scales[8] (56 bytes); lane g = 16-weight block g
 struct KIQ1M : Iq8Tab<2048> {
-    static constexpr int BS = QK, G = 16, N = 16, BB = 56;
+    static constexpr int BS = QK, G = 16, N = 16, BB = 56, WS = COOP_WS_BYTES;
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
                           const QParams &p) {
         const uint64_t *grid = Iq8Tab<2048>::grid(lds);
@@ -229,7 +253,8 @@ struct KIQ1M : Iq8Tab<2048> {
         bool live = false;
         int best_k = 0;       // the shift combination (0 for a skipped block, masks[0] = 0)
         float scale = 0.f;
-        int gi2[2] = {0, 0};
+        int gi2[2] = {0, 0}, mk2[2] = {0, 0};
+        CoopWS &ws = *(CoopWS *)wave_ws<KIQ1M>(img);
         if (!(mx < EPS_IQ1M)) {
             Lv<N> R;
             stable_ranks<N>(x, R);
@@ -299,10 +324,8 @@ struct KIQ1M : Iq8Tab<2048> {
                 const bool flip = scale < 0;
                 if (flip) { scale = -scale; bk = 3 - bk; }
                 best_k = bk;
-                bool all_on_grid = true;
 #pragma unroll
                 for (int k = 0; k < 2; ++k) {
-                    const bool minus = k == 0 ? !(bk < 2) : !(bk % 2 == 0);
                     int k3 = 0, p3 = 1;
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
@@ -312,15 +335,22 @@ struct KIQ1M : Iq8Tab<2048> {
                         k3 += l * p3;
                         p3 *= 3;
                     }
-                    const int m = map3[k3];
-                    int gi = m;
-                    if (m < 0) {
-                        all_on_grid = false;
-                        gi = nb_best_iq1(p.neigh + m3_off(m), grid, x + 8 * k, weight + 8 * k, scale, minus);
-                        if (gi < 0) { flag_err(p); gi = 0; }
-                    }
-                    gi2[k] = gi;
+                    mk2[k] = map3[k3];
                 }
+            }
+        }
+        // the groups' points (every lane: the neighbour search is wave-wide)
+        bool all_on_grid = true;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const bool minus = k == 0 ? !(best_k < 2) : !(best_k % 2 == 0);
+            bool og;
+            gi2[k] = iq1_group_point(live, mk2[k], x + 8 * k, weight + 8 * k, scale, minus, p, grid, ws, og);
+            all_on_grid = all_on_grid && og;
+        }
+        if (live) {
+            {
+                const int bk = best_k;
                 if (!all_on_grid) {
                     float sqx = 0, sq2 = 0;
 #pragma unroll
