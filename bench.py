@@ -36,6 +36,22 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+def pmc_traffic(key):
+    """HBM bytes per launch of a kernel as measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on this workload and
+    scaled by the same counters' reading for a copy kernel of known size (profiles/hbm_traffic_pmc.md; the lines
+    `traffic[<key>] = <bytes>`), or None when not measured"""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_pmc.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                line = line.strip().strip("`")
+                if line.startswith("traffic[%s] = " % key):
+                    return int(line.split("=", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_threads():
     try:
         return max(1, min(len(os.sched_getaffinity(0)), 64))
@@ -229,7 +245,7 @@ def host_sample(torch, wl, rows):
     return wl.raw.reshape(-1)[: rows * wl.ncol // 32 * 17].cpu().numpy()
 
 
-def cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, wl, typ, ms, out_dev, sample_rows, want_cpu):
+def cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, wl, typ, ms, out_dev, sample_rows, want_cpu, tkey=None):
     """the CPU baseline on a sample, the op count per weight, and a byte spot check of the GPU output"""
     import numpy as np
     nthr = cpu_threads()
@@ -260,8 +276,8 @@ def cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, wl, typ, ms, out_dev, sample
         bpw = {0: 4.0, 30: 2.0}.get(wl.src, 17 / 32) + 34 / 32
         achieved = bpw * n_total / (ms / 1e3) / 1e9
         entry["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                             "algorithmic_bytes_per_weight": bpw}
+                             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": pmc_traffic(tkey),
+                             "algorithmic_bytes_per_weight": bpw, "algorithmic_bytes": round(bpw * n_total)}
     else:
         ops_rows = min(sample_rows, 64)
         sub = raw[: (ops_rows * wl.ncol) * {0: 4, 30: 2}.get(wl.src, 0)] if wl.src in (0, 30) else \
@@ -272,7 +288,7 @@ def cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, wl, typ, ms, out_dev, sample
         opw = orc_ops.ops_read_reset() / (ops_rows * wl.ncol)
         achieved = opw * n_total / (ms / 1e3) / 1e12
         entry["roofline"] = {"bound": "valu", "achieved": round(achieved, 3), "peak": VALU_PEAK_TOPS,
-                             "unit": "Tops/s", "frac": round(achieved / VALU_PEAK_TOPS, 4), "traffic": None,
+                             "unit": "Tops/s", "frac": round(achieved / VALU_PEAK_TOPS, 4), "traffic": pmc_traffic(tkey),
                              "algorithmic_ops_per_weight": round(opw, 1)}
     return entry
 
@@ -302,7 +318,8 @@ def main():
     c2 = wl_c2(torch, gpuq)
     log("headline: Q4_K on %s" % c2.name)
     ms, out = time_gpu(torch, gq, gpuq, c2, gpuq.Q4_K, args.steps, args.warmup)
-    head = cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, c2, gpuq.Q4_K, ms, out, c2.nrow, not args.no_cpu)
+    head = cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, c2, gpuq.Q4_K, ms, out, c2.nrow, not args.no_cpu,
+                            "Q4_K BF16 2048x7168")
     value = c2.n / (ms / 1e3) / 1e6
     line = {"metric": METRIC, "value": round(value, 1), "unit": "Mweights/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
@@ -324,7 +341,8 @@ def main():
             ms_t, out_t = time_gpu(torch, gq, gpuq, wl, typ, k, args.warmup)
             e = {"workload": wl.name, "value": round(wl.n / (ms_t / 1e3) / 1e6, 1), "unit": "Mweights/s",
                  "ms_per_step": round(ms_t, 4), "steps": k}
-            e.update(cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, wl, typ, ms_t, out_t, srows, not args.no_cpu))
+            e.update(cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, wl, typ, ms_t, out_t, srows, not args.no_cpu,
+                                      "%s %s" % (name, "F32 4096x4096" if wl is c1 else "BF16 2048x7168")))
             per[name] = e
             del out_t
         del c1

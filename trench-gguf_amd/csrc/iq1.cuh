@@ -125,7 +125,9 @@ struct KIQ1S : Iq8Tab<2048> {
         if (!(mx < EPS_IQ1S)) {
             Lv<N> R;
             stable_ranks<N>(x, R);
-            float sumx[N + 1], sumw[N + 1];
+            // prefix sums 0..N: entries 0..N-1 in 32-register arrays (their loop-uniform indexing stays in registers;
+            // a 33-entry array would not) and entry N, the totals, apart
+            float sumx[N], sumw[N], totx, totw;
             sumx[0] = sumw[0] = 0;
 #pragma unroll
             for (int j = 0; j < N; ++j) {
@@ -133,26 +135,31 @@ struct KIQ1S : Iq8Tab<2048> {
 #pragma unroll
                 for (int i = 0; i < N; ++i)
                     if (R.get(i) == (uint32_t)j) { tx = weight[i] * x[i]; tw = weight[i]; }
-                sumx[j + 1] = sumx[j] + tx;
-                sumw[j + 1] = sumw[j] + tw;
+                if (j + 1 < N) {
+                    sumx[j + 1] = sumx[j] + tx;
+                    sumw[j + 1] = sumw[j] + tw;
+                } else {
+                    totx = sumx[j] + tx;
+                    totw = sumw[j] + tw;
+                }
             }
             float best_score = -FLT_MAX;
             scale = mx;
             int besti1 = -1, besti2 = -1, best_shift = 0;
             for (int i1 = 0; i1 <= N; ++i1) {
-                const float a_x = sumx[i1] - sumx[0], a_w = sumw[i1] - sumw[0];
-                const float s1x = sumx[i1], s1w = sumw[i1];
+                const float s1x = i1 < N ? sumx[i1 & (N - 1)] : totx, s1w = i1 < N ? sumw[i1 & (N - 1)] : totw;
+                const float a_x = s1x - sumx[0], a_w = s1w - sumw[0];
                 for (int i2 = i1; i2 <= N; ++i2) {
-                    const float s2x = sumx[i2], s2w = sumw[i2];
-                    float sumqx = a_x * xp0 + (s2x - s1x) * xp1 + (sumx[N] - s2x) * xp2;
-                    float sumq2 = a_w * xp0 * xp0 + (s2w - s1w) * xp1 * xp1 + (sumw[N] - s2w) * xp2 * xp2;
+                    const float s2x = i2 < N ? sumx[i2 & (N - 1)] : totx, s2w = i2 < N ? sumw[i2 & (N - 1)] : totw;
+                    float sumqx = a_x * xp0 + (s2x - s1x) * xp1 + (totx - s2x) * xp2;
+                    float sumq2 = a_w * xp0 * xp0 + (s2w - s1w) * xp1 * xp1 + (totw - s2w) * xp2 * xp2;
                     if (sumq2 > 0 && sumqx * sumqx > best_score * sumq2) {
                         scale = sumqx / sumq2;
                         best_score = scale * sumqx;
                         besti1 = i1; besti2 = i2; best_shift = 1;
                     }
-                    sumqx = a_x * xm0 + (s2x - s1x) * xm1 + (sumx[N] - s2x) * xm2;
-                    sumq2 = a_w * xm0 * xm0 + (s2w - s1w) * xm1 * xm1 + (sumw[N] - s2w) * xm2 * xm2;
+                    sumqx = a_x * xm0 + (s2x - s1x) * xm1 + (totx - s2x) * xm2;
+                    sumq2 = a_w * xm0 * xm0 + (s2w - s1w) * xm1 * xm1 + (totw - s2w) * xm2 * xm2;
                     if (sumq2 > 0 && sumqx * sumqx > best_score * sumq2) {
                         scale = sumqx / sumq2;
                         best_score = scale * sumqx;
