@@ -39,7 +39,7 @@ def log(msg):
 def pmc_traffic(key):
     """HBM bytes per launch of a kernel as measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on this workload and
     scaled by the same counters' reading for a copy kernel of known size (profiles/hbm_traffic_pmc.md; the lines
-    `traffic[<key>] = <bytes>`), or None when not measured"""
+    `traffic[<key>] = <bytes>`; keys ending in "expert" are per expert of a batch), or None when not measured"""
     path = os.path.join(ROOT, "profiles", "hbm_traffic_pmc.md")
     try:
         with open(path) as f:
@@ -245,7 +245,8 @@ def host_sample(torch, wl, rows):
     return wl.raw.reshape(-1)[: rows * wl.ncol // 32 * 17].cpu().numpy()
 
 
-def cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, wl, typ, ms, out_dev, sample_rows, want_cpu, tkey=None):
+def cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, wl, typ, ms, out_dev, sample_rows, want_cpu, tkey=None,
+                     tscale=1):
     """the CPU baseline on a sample, the op count per weight, and a byte spot check of the GPU output"""
     import numpy as np
     nthr = cpu_threads()
@@ -272,11 +273,14 @@ def cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, wl, typ, ms, out_dev, sample
                                            % (sample_rows, wl.ncol, n / 1e6, cpu_s, nthr)}
     # roofline
     n_total = wl.n
+    traffic = pmc_traffic(tkey)
+    if traffic is not None:
+        traffic *= tscale
     if typ == gpuq.Q8_0:
         bpw = {0: 4.0, 30: 2.0}.get(wl.src, 17 / 32) + 34 / 32
         achieved = bpw * n_total / (ms / 1e3) / 1e9
         entry["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": pmc_traffic(tkey),
+                             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                              "algorithmic_bytes_per_weight": bpw, "algorithmic_bytes": round(bpw * n_total)}
     else:
         ops_rows = min(sample_rows, 64)
@@ -288,7 +292,7 @@ def cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, wl, typ, ms, out_dev, sample
         opw = orc_ops.ops_read_reset() / (ops_rows * wl.ncol)
         achieved = opw * n_total / (ms / 1e3) / 1e12
         entry["roofline"] = {"bound": "valu", "achieved": round(achieved, 3), "peak": VALU_PEAK_TOPS,
-                             "unit": "Tops/s", "frac": round(achieved / VALU_PEAK_TOPS, 4), "traffic": pmc_traffic(tkey),
+                             "unit": "Tops/s", "frac": round(achieved / VALU_PEAK_TOPS, 4), "traffic": traffic,
                              "algorithmic_ops_per_weight": round(opw, 1)}
     return entry
 
@@ -355,7 +359,8 @@ def main():
             e = {"workload": c3.name, "value": round(c3.n / (ms_t / 1e3) / 1e6, 1), "unit": "Mweights/s",
                  "ms_per_step": round(ms_t, 3), "steps": ksteps}
             srows = c3.nrow * min(nexp_c3, max(2, nthr))
-            e.update(cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, c3, typ, ms_t, out_t, srows, not args.no_cpu))
+            e.update(cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, c3, typ, ms_t, out_t, srows, not args.no_cpu,
+                                      "%s BF16 2048x7168 expert" % name, c3.nmat))
             if "cpu_baseline" in e:
                 e["speedup_vs_cpu"] = round(e["value"] / e["cpu_baseline"]["value"], 1)
             per[name] = e
@@ -370,7 +375,8 @@ def main():
             e = {"workload": c4.name, "value": round(c4.n / (ms_t / 1e3) / 1e6, 1), "unit": "Mweights/s",
                  "ms_per_step": round(ms_t, 3), "steps": ksteps}
             srows = c4.nrow * min(nexp_c4, max(2, nthr))
-            e.update(cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, c4, typ, ms_t, out_t, srows, not args.no_cpu))
+            e.update(cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, c4, typ, ms_t, out_t, srows, not args.no_cpu,
+                                      "%s MXFP4 2048x7168 expert" % name, c4.nmat))
             if "cpu_baseline" in e:
                 e["speedup_vs_cpu"] = round(e["value"] / e["cpu_baseline"]["value"], 1)
             per[name] = e
