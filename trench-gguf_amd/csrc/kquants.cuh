@@ -594,7 +594,12 @@ struct KQ6K {
 
 // ------------------------------------------------------------------ Q8_0 (gpuq/gpuq.hip:1831-1838)
 // block: d qs[32] (34 bytes). Streaming sources (F32 / F16 / BF16): every lane loads 16 contiguous bytes a step, so
-// a wave reads 1 KB contiguous per load instruction; 32/E lanes share a block's amax through xor shuffles.
+// a wave reads 1 KB contiguous per load instruction; 32/E lanes share a block's amax through xor shuffles. The
+// source is read once: nontemporal loads.
+DEV uint4 nt_load16(const uint8_t *p) {
+    const v4u32 v = __builtin_nontemporal_load((const v4u32 *)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 template <int SRC> __global__ __launch_bounds__(WG_THREADS) void k_q8_0_stream(const uint8_t *src, uint8_t *dst,
                                                                                int64_t nblk) {
     constexpr int E = SRC == T_F32 ? 4 : 8;          // values a lane loads a step
@@ -615,7 +620,7 @@ template <int SRC> __global__ __launch_bounds__(WG_THREADS) void k_q8_0_stream(c
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int64_t blk = b0 + u * BPS + bl;
-            raw[u] = blk < nblk ? *(const uint4 *)(src + (blk * 32 + part * E) * (SRC == T_F32 ? 4 : 2))
+            raw[u] = blk < nblk ? nt_load16(src + (blk * 32 + part * E) * (SRC == T_F32 ? 4 : 2))
                                 : make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
