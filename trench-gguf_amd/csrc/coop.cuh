@@ -71,7 +71,10 @@ DEV int wave_incl_scan(int v) {
 // Rounds run in chunks of up to 8: a first pass walks the chunk's positions (owner, list position) and issues their
 // list reads, a second reads their grid points, a third evaluates them, so a chunk's reads are in flight together.
 template <class Eval>
-DEV int coop_search(int cnt, int off, float scale, const uint16_t *neigh, CoopWS &ws, const Eval &ev) {
+DEV int coop_search(int cnt, int off, float scale, const uint16_t *neigh, int neigh_len, CoopWS &ws,
+                    const Eval &ev) {
+    // the lists through a buffer resource: 32-bit offsets, and reads past the table return 0 instead of faulting
+    const __amdgpu_buffer_rsrc_t nrs = __builtin_amdgcn_make_buffer_rsrc((void *)neigh, 0, neigh_len * 2, 0x00020000);
     const int lane = lane_id();
     const int incl = wave_incl_scan(cnt);
     const int total = __builtin_amdgcn_readlane(incl, 63);
@@ -96,9 +99,8 @@ DEV int coop_search(int cnt, int off, float scale, const uint16_t *neigh, CoopWS
     if (np == 0) o = 63 - __clzll(has);                 // (idle lane: repeats the last owner's candidates)
     int4 oi = ws.info[o];
     int ocnt = oi.w & 0xffff;
-    const uint16_t *ol = neigh + oi.x + 1;
+    int ol = oi.x + 1;                                  // the owner's first list entry
     int j = np ? p0 - oi.y : 0;
-    int4 ni = ws.info[oi.w >> 16];                      // the next owner's entry, read ahead of its use
     // evaluation state: the owner whose values are in registers, and the running minimum over its candidates
     int cur = -1;
     float st[16], sc = 0.f;
@@ -114,15 +116,14 @@ DEV int coop_search(int cnt, int off, float scale, const uint16_t *neigh, CoopWS
             if (r < rend) {
                 if (j >= ocnt && r0 + r < np) {         // the owner's list ends: on to the next lane with a list
                     o = oi.w >> 16;
-                    oi = ni;
+                    oi = ws.info[o];
                     ocnt = oi.w & 0xffff;
-                    ol = neigh + oi.x + 1;
+                    ol = oi.x + 1;
                     j = 0;
-                    ni = ws.info[oi.w >> 16];           // (not needed before the next change of owner)
                 }
                 const int jc = j < ocnt ? j : ocnt - 1;
                 own_j[r] = o | (jc << 6);
-                idx[r] = ol[jc];
+                idx[r] = __builtin_amdgcn_raw_buffer_load_b16(nrs, (ol + jc) * 2, 0, 0);
                 ++j;
             }
         }

@@ -57,7 +57,7 @@ DEV int iq1_group_point(bool live, int m, const float *xk, const float *wk, floa
     on_grid = !srch;
     const int cnt = srch ? m3_cnt(m) : 0, off = srch ? m3_off(m) : 0;
     if (srch) coop_stage<8>(ws, xk, wk);
-    const int gi = coop_search(cnt, off, minus ? -scale : scale, p.neigh, ws, EvalIq1{grid});
+    const int gi = coop_search(cnt, off, minus ? -scale : scale, p.neigh, p.neigh_len, ws, EvalIq1{grid});
     if (!live) return 0;
     if (!srch) return m;
     if (gi < 0) {

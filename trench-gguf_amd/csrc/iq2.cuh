@@ -79,7 +79,7 @@ DEV int group_point_s(bool active, int k3, const int32_t *map3, const QParams &p
     const bool srch = active && m < 0;
     const int off = srch ? m3_off(m) : 0;
     const int cnt = srch ? m3_cnt(m) : 0;
-    const int gi = coop_search(cnt, off, scale, p.neigh, ws, EvalIq8{grid});
+    const int gi = coop_search(cnt, off, scale, p.neigh, p.neigh_len, ws, EvalIq8{grid});
     if (!srch) return active ? m : 0;
     if (gi < 0) {
         flag_err(p);
@@ -192,6 +192,12 @@ struct KIQ2XXS : Iq8Tab<256> {
         // The trials' groups, group by group (every lane runs them: the neighbour search is wave-wide): a group's
         // values are staged once for its 13 trial scales, and trial t's grid index of group k goes to byte k of
         // gtab[t]. Each trial's searches do not depend on another trial's outcome, so the order changes nothing.
+        float idv[NTRIAL], tsv[NTRIAL];         // the trial scales' inverse and scale, indexed by a uniform trial
+#pragma unroll
+        for (int t = 0; t < NTRIAL; ++t) {
+            idv[t] = (5 + (t - 6) * 0.1f) / eff_max;
+            tsv[t] = 1 / idv[t];
+        }
 #pragma unroll 1
         for (int k = 0; k < 4; ++k) {           // (not unrolled: one copy of the search code, groups kept apart)
             const float *xk = xval;            // group k: rotated to the front (rot8 below)
@@ -201,8 +207,7 @@ struct KIQ2XXS : Iq8Tab<256> {
             coop_stage<8>(ws, xk, waux);
 #pragma unroll 1
             for (int t = 0; t < NTRIAL; ++t) {
-                const float id = (5 + (t - 6) * 0.1f) / eff_max;
-                const float this_scale = 1 / id;
+                const float id = idv[t], this_scale = tsv[t];
                 bool og;
                 const int gi = group_point_s(live, group_key3(xk, id), map3, p, grid, this_scale, ws, og);
                 ((uint8_t *)(gtab + t * 64))[k] = (uint8_t)gi;
