@@ -42,9 +42,20 @@ template <int NV> DEV void coop_stage(CoopWS &ws, const float *xv, const float *
     }
 }
 
-// a / b for 0 <= a < 2^20, 1 <= b < 2^12: a float quotient, corrected to the floor
+// an owner's staged values into registers
+DEV void coop_fetch(const CoopWS &ws, int owner, float (&st)[16]) {
+    const float4 *sp = (const float4 *)ws.stage[owner];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float4 v = sp[i];
+        st[4 * i] = v.x; st[4 * i + 1] = v.y; st[4 * i + 2] = v.z; st[4 * i + 3] = v.w;
+    }
+}
+
+// a / b for 0 <= a < 2^20, 1 <= b < 2^12: a float quotient (hardware reciprocal, within 1 of the floor), corrected
+// to the floor
 DEV int div_small(int a, int b) {
-    int q = (int)((float)a * (1.0f / (float)b));
+    int q = (int)((float)a * __builtin_amdgcn_rcpf((float)b));
     q += (q + 1) * b <= a;
     q -= q * b > a;
     return q;
@@ -102,9 +113,10 @@ DEV int coop_search(int cnt, int off, float scale, const uint16_t *neigh, int ne
     int ol = oi.x + 1;                                  // the owner's first list entry
     int j = np ? p0 - oi.y : 0;
     // evaluation state: the owner whose values are in registers, and the running minimum over its candidates
-    int cur = -1;
-    float st[16], sc = 0.f;
+    int cur = o;
+    float st[16], sc = __int_as_float(oi.z);
     unsigned long long kmin = ~0ull;
+    coop_fetch(ws, o, st);
     for (int r0 = 0; r0 < R; r0 += 8) {
         const int rend = R - r0 < 8 ? R - r0 : 8;
         int own_j[8], idx[8];           // owner | list position << 6; the candidate's grid index
@@ -135,15 +147,10 @@ DEV int coop_search(int cnt, int off, float scale, const uint16_t *neigh, int ne
             if (r < rend) {
                 const int owner = own_j[r] & 63;
                 if (owner != cur) {
-                    if (cur >= 0) atomicMin(&ws.key[cur], kmin);
+                    atomicMin(&ws.key[cur], kmin);
                     cur = owner;
                     kmin = ~0ull;
-                    const float4 *sp = (const float4 *)ws.stage[owner];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float4 v = sp[i];
-                        st[4 * i] = v.x; st[4 * i + 1] = v.y; st[4 * i + 2] = v.z; st[4 * i + 3] = v.w;
-                    }
+                    coop_fetch(ws, owner, st);
                     sc = __int_as_float(ws.info[owner].z);
                 }
                 const float d2 = ev(st, sc, pt[r]);
@@ -153,7 +160,7 @@ DEV int coop_search(int cnt, int off, float scale, const uint16_t *neigh, int ne
             }
         }
     }
-    if (cur >= 0) atomicMin(&ws.key[cur], kmin);
+    atomicMin(&ws.key[cur], kmin);
     wave_sync();
     if (cnt <= 0) return -2;
     const unsigned long long k = ws.key[lane];
