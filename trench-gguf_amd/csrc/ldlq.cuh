@@ -6,11 +6,14 @@
 //   2. k_ldlq_solve, one lane a row: E = blk - to_float(block bytes) in f32, then Es = E U_BB^-1 by forward
 //      substitution in f64: Es[j] = (E[j] - sum_{i<j} Es[i] U[c0+i][c0+j]) / U[c0+j][c0+j], each sum a fused
 //      multiply-add chain over i in ascending order;
-//   3. k_ldlq_update, a register-tiled f64 GEMM: W[r][c] -= (float)(sum_{i<256} Es[r][i] U[c0+i][c]) for the later
-//      columns c, each output a fused multiply-add chain over i in ascending order from 0.0.
+//   3. k_ldlq_update, an f64 GEMM on the matrix cores: W[r][c] -= (float)(sum_{i<256} Es[r][i] U[c0+i][c]) for the
+//      later columns c, each output a fused multiply-add chain over i in ascending order from 0.0.
 // The reference leaves the order of those sums to LAPACK / BLAS (numpy's LU solve, torch's solve_triangular and
 // GEMM); this library fixes it as above, and its CPU oracle computes the same chains, so the bytes are reproducible
-// on any hardware. The f64 work runs on VALU v_fma_f64, whose rate on gfx950 equals the f64 MFMA peak.
+// on any hardware. v_mfma_f64_16x16x4f64 accumulates its four products into each output as four IEEE fused
+// multiply-adds in k order (checked bit for bit on gfx950 against a sequential fma chain, subnormal results
+// included), so a chain of them over k = 0, 4, ..., 252 is exactly the ascending fma chain; its output layout is
+// lane l, element e -> row 4e + l/16, column l%16.
 #pragma once
 #include "dequant.cuh"
 
@@ -62,8 +65,11 @@ __global__ __launch_bounds__(64) void k_ldlq_solve(const float *__restrict__ W, 
     }
 }
 
-// W[m][row][c] -= (float)(Es[m*ne1+row][:] . U_m[c0 .. c0+255][c]) for c in [c0 + 256, ne0)
-__global__ __launch_bounds__(256) void k_ldlq_update(float *__restrict__ W, const double *__restrict__ Es,
+// W[m][row][c] -= (float)(Es[m*ne1+row][:] . U_m[c0 .. c0+255][c]) for c in [c0 + 256, ne0). A workgroup of 4 waves
+// owns a 128 x 128 tile (each wave 64 x 64: 4 x 4 MFMA tiles of 16 x 16); k runs in chunks of 16 staged in LDS
+// (k-major, padded rows) and 4 MFMA k-steps a chunk.
+typedef double ldlq_d4 __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_ldlq_update(float *__restrict__ W, const double *__restrict__ Es,
                                                      const double *__restrict__ U, int64_t u_stride, int64_t ne1,
                                                      int64_t ne0, int64_t c0) {
     __shared__ __align__(16) double As[LDLQ_BK][LDLQ_TM + 2];
@@ -72,50 +78,62 @@ __global__ __launch_bounds__(256) void k_ldlq_update(float *__restrict__ W, cons
     const int64_t row0 = (int64_t)blockIdx.y * LDLQ_TM;
     const int64_t col0 = c0 + QK + (int64_t)blockIdx.x * LDLQ_TN;
     const double *Um = U + m * u_stride;
-    const int tid = threadIdx.x, tx = tid % 16, ty = tid / 16;
-    double acc[8][8];
+    const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+    const int wr0 = (wave >> 1) * 64, wc0 = (wave & 1) * 64;   // the wave's 64 x 64 sub-tile
+    ldlq_d4 acc[4][4];
 #pragma unroll
-    for (int a = 0; a < 8; ++a)
+    for (int a = 0; a < 4; ++a)
 #pragma unroll
-        for (int b = 0; b < 8; ++b) acc[a][b] = 0.0;
+        for (int b = 0; b < 4; ++b) acc[a][b] = ldlq_d4{0.0, 0.0, 0.0, 0.0};
     // loader roles: A: row tid/2, k half (tid%2)*8; B: k row tid/16, columns 8*(tid%16)
     const int ar = tid / 2, ak = (tid % 2) * 8;
     const int bk = tid / 16, bc = 8 * (tid % 16);
     const bool a_ok = row0 + ar < ne1;
     const double *arow = Es + (m * ne1 + (a_ok ? row0 + ar : 0)) * QK;
-    for (int k0 = 0; k0 < QK; k0 += LDLQ_BK) {
-        double av[8], bv[8];
+    // the next chunk's global reads are issued before the current chunk's MFMAs, so they overlap
+    double av[8], bv[8];
+    auto load = [&](int k0) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) av[j] = a_ok ? arow[k0 + ak + j] : 0.0;
         const double *brow = Um + (c0 + k0 + bk) * ne0;
 #pragma unroll
         for (int j = 0; j < 8; ++j) bv[j] = col0 + bc + j < ne0 ? brow[col0 + bc + j] : 0.0;
+    };
+    load(0);
+    for (int k0 = 0; k0 < QK; k0 += LDLQ_BK) {
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < 8; ++j) As[ak + j][ar] = av[j];
 #pragma unroll
         for (int j = 0; j < 8; ++j) Bs[bk][bc + j] = bv[j];
         __syncthreads();
+        if (k0 + LDLQ_BK < QK) load(k0 + LDLQ_BK);
 #pragma unroll
-        for (int kk = 0; kk < LDLQ_BK; ++kk) {
-            double a[8], b[8];
+        for (int ks = 0; ks < LDLQ_BK; ks += 4) {
+            const int kk = ks + lane / 16;
+            double a[4], b[4];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) { a[j] = As[kk][8 * ty + j]; b[j] = Bs[kk][8 * tx + j]; }
+            for (int t = 0; t < 4; ++t) {
+                a[t] = As[kk][wr0 + 16 * t + lane % 16];
+                b[t] = Bs[kk][wc0 + 16 * t + lane % 16];
+            }
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
+            for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) acc[i][j] = fma(a[i], b[j], acc[i][j]);
+                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[i], b[j], acc[i][j], 0, 0, 0);
         }
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int64_t row = row0 + 8 * ty + i;
-        if (row >= ne1) continue;
-        float *wr = W + (m * ne1 + row) * ne0;
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int64_t col = col0 + 8 * tx + j;
-            if (col < ne0) wr[col] = wr[col] - (float)acc[i][j];
+        for (int e = 0; e < 4; ++e) {
+            const int64_t row = row0 + wr0 + 16 * i + 4 * e + lane / 16;
+            if (row >= ne1) continue;
+            float *wr = W + (m * ne1 + row) * ne0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int64_t col = col0 + wc0 + 16 * j + lane % 16;
+                if (col < ne0) wr[col] = wr[col] - (float)acc[i][j][e];
+            }
         }
-    }
 }
