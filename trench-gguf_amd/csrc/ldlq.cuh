@@ -17,7 +17,9 @@
 #pragma once
 #include "dequant.cuh"
 
+#ifndef LDLQ_BK
 #define LDLQ_BK 16            // k-chunk of the update GEMM
+#endif
 #define LDLQ_TM 128           // update tile rows
 #define LDLQ_TN 128           // update tile columns
 
@@ -85,27 +87,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     for (int a = 0; a < 4; ++a)
 #pragma unroll
         for (int b = 0; b < 4; ++b) acc[a][b] = ldlq_d4{0.0, 0.0, 0.0, 0.0};
-    // loader roles: A: row tid/2, k half (tid%2)*8; B: k row tid/16, columns 8*(tid%16)
-    const int ar = tid / 2, ak = (tid % 2) * 8;
-    const int bk = tid / 16, bc = 8 * (tid % 16);
+    // loader roles (E = BK/2 values a thread a tile): A: row tid/2, k half (tid%2)*E; B: k row tid/(128/E), columns
+    // E*(tid%(128/E))
+    constexpr int E = LDLQ_BK / 2, BPR = LDLQ_TN / E;
+    const int ar = tid / 2, ak = (tid % 2) * E;
+    const int bk = tid / BPR, bc = E * (tid % BPR);
     const bool a_ok = row0 + ar < ne1;
     const double *arow = Es + (m * ne1 + (a_ok ? row0 + ar : 0)) * QK;
     // the next chunk's global reads are issued before the current chunk's MFMAs, so they overlap
-    double av[8], bv[8];
+    double av[E], bv[E];
     auto load = [&](int k0) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) av[j] = a_ok ? arow[k0 + ak + j] : 0.0;
+        for (int j = 0; j < E; ++j) av[j] = a_ok ? arow[k0 + ak + j] : 0.0;
         const double *brow = Um + (c0 + k0 + bk) * ne0;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) bv[j] = col0 + bc + j < ne0 ? brow[col0 + bc + j] : 0.0;
+        for (int j = 0; j < E; ++j) bv[j] = col0 + bc + j < ne0 ? brow[col0 + bc + j] : 0.0;
     };
     load(0);
     for (int k0 = 0; k0 < QK; k0 += LDLQ_BK) {
         __syncthreads();
 #pragma unroll
-        for (int j = 0; j < 8; ++j) As[ak + j][ar] = av[j];
+        for (int j = 0; j < E; ++j) As[ak + j][ar] = av[j];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) Bs[bk][bc + j] = bv[j];
+        for (int j = 0; j < E; ++j) Bs[bk][bc + j] = bv[j];
         __syncthreads();
         if (k0 + LDLQ_BK < QK) load(k0 + LDLQ_BK);
 #pragma unroll
