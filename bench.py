@@ -39,7 +39,7 @@ def log(msg):
 def pmc_traffic(key):
     """HBM bytes per launch of a kernel as measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on this workload and
     scaled by the same counters' reading for a copy kernel of known size (profiles/hbm_traffic_pmc.md; the lines
-    `traffic[<key>] = <bytes>`; keys ending in "expert" are per expert of a batch), or None when not measured"""
+    `traffic[<key>] = <bytes>`), or None when not measured on this workload"""
     path = os.path.join(ROOT, "profiles", "hbm_traffic_pmc.md")
     try:
         with open(path) as f:
@@ -360,7 +360,7 @@ def main():
                  "ms_per_step": round(ms_t, 3), "steps": ksteps}
             srows = c3.nrow * min(nexp_c3, max(2, nthr))
             e.update(cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, c3, typ, ms_t, out_t, srows, not args.no_cpu,
-                                      "%s BF16 2048x7168 expert" % name, c3.nmat))
+                                      "%s BF16 %dx2048x7168" % (name, c3.nmat)))
             if "cpu_baseline" in e:
                 e["speedup_vs_cpu"] = round(e["value"] / e["cpu_baseline"]["value"], 1)
             per[name] = e
@@ -376,7 +376,7 @@ def main():
                  "ms_per_step": round(ms_t, 3), "steps": ksteps}
             srows = c4.nrow * min(nexp_c4, max(2, nthr))
             e.update(cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, c4, typ, ms_t, out_t, srows, not args.no_cpu,
-                                      "%s MXFP4 2048x7168 expert" % name, c4.nmat))
+                                      "%s MXFP4 %dx2048x7168" % (name, c4.nmat)))
             if "cpu_baseline" in e:
                 e["speedup_vs_cpu"] = round(e["value"] / e["cpu_baseline"]["value"], 1)
             per[name] = e

@@ -78,12 +78,16 @@ DEV void img_zero(uint8_t *img, int nbytes) {
 typedef unsigned int v4u32 __attribute__((ext_vector_type(4)));
 
 // copy nbytes (even) of the image to global dst (2-byte aligned) with coalesced stores: 16 bytes a lane when dst and
-// nbytes allow it, else dwords. Output blocks are written once and not read back, so the stores are nontemporal.
-DEV void img_store(uint8_t *dst, const uint8_t *img, int nbytes) {
+// nbytes allow it, else dwords. NT: nontemporal stores (the Q8_0 stream, whose tiles are whole 16-byte runs; for
+// tiles that end inside a cache line they raise the written bytes, the L2 no longer merging neighbouring tiles).
+template <bool NT = false> DEV void img_store(uint8_t *dst, const uint8_t *img, int nbytes) {
     const int lane = lane_id();
     if ((((uintptr_t)dst) & 15) == 0 && (nbytes & 15) == 0) {
-        for (int i = lane; i < nbytes / 16; i += 64)
-            __builtin_nontemporal_store(*(const v4u32 *)(img + 16 * i), (v4u32 *)(dst + 16 * i));
+        for (int i = lane; i < nbytes / 16; i += 64) {
+            const v4u32 v = *(const v4u32 *)(img + 16 * i);
+            if (NT) __builtin_nontemporal_store(v, (v4u32 *)(dst + 16 * i));
+            else *(v4u32 *)(dst + 16 * i) = v;
+        }
         return;
     }
     int head = ((uintptr_t)dst & 3) ? 2 : 0;            // dst is at least 2-byte aligned
@@ -95,7 +99,8 @@ DEV void img_store(uint8_t *dst, const uint8_t *img, int nbytes) {
         uint32_t v;
         if (head) v = (uint32_t)*(const uint16_t *)s | ((uint32_t)*(const uint16_t *)(s + 2) << 16);
         else v = *(const uint32_t *)s;
-        __builtin_nontemporal_store(v, (uint32_t *)(dst + head + 4 * i));
+        if (NT) __builtin_nontemporal_store(v, (uint32_t *)(dst + head + 4 * i));
+        else *(uint32_t *)(dst + head + 4 * i) = v;
     }
     const int tail = nbytes - head - 4 * nw;             // 0 or 2
     if (tail && lane == 0) *(uint16_t *)(dst + nbytes - 2) = *(const uint16_t *)(img + nbytes - 2);

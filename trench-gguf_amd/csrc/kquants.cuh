@@ -650,7 +650,7 @@ template <int SRC> __global__ __launch_bounds__(WG_THREADS) void k_q8_0_stream(c
             }
         }
         wave_sync();
-        img_store(dst + b0 * 34, img, nact * 34);
+        img_store<true>(dst + b0 * 34, img, nact * 34);
         wave_sync();
     }
 }
