@@ -27,6 +27,7 @@
 struct CoopWS {
     float stage[64][16];        // an owner's values: 8 (or 4) x's then 8 (or 4) weights
     int4 info[64];              // owner: list offset, first position, scale bits, list length | next owner << 16
+    int2 nxt[64];               // owner: its next owner's list offset, list length | the one after it << 16
     unsigned long long key[64]; // owner: min of (distance bits << 32 | list position << 12 | grid index)
     uint8_t mark[64];           // lane: the owner of its first position
 };
@@ -95,6 +96,10 @@ DEV int coop_search(int cnt, int off, float scale, const uint16_t *neigh, int ne
     const unsigned long long after = has & ~((2ull << lane) - 1);
     const int next = after ? __ffsll((long long)after) - 1 : lane;     // the next lane with a list
     ws.info[lane] = make_int4(off, excl, __float_as_int(scale), cnt | (next << 16));
+    {
+        const int noff = __shfl(off, next), ncnt = __shfl(cnt, next), nnext = __shfl(next, next);
+        ws.nxt[lane] = make_int2(noff, ncnt | (nnext << 16));
+    }
     ws.key[lane] = ~0ull;
     const int R = (total + 63) >> 6;                    // positions a lane
     if (cnt > 0) {                                      // lanes L with excl <= L*R < incl start in this list
@@ -108,9 +113,11 @@ DEV int coop_search(int cnt, int off, float scale, const uint16_t *neigh, int ne
     // walk state: owner, list position, the owner's list length and its first entry
     int o = ws.mark[lane] & 63;
     if (np == 0) o = 63 - __clzll(has);                 // (idle lane: repeats the last owner's candidates)
-    int4 oi = ws.info[o];
+    const int4 oi = ws.info[o];
     int ocnt = oi.w & 0xffff;
     int ol = oi.x + 1;                                  // the owner's first list entry
+    int onext = oi.w >> 16;                             // the owner after it, and that owner's list (read ahead)
+    int2 nx = ws.nxt[o];
     int j = np ? p0 - oi.y : 0;
     // evaluation state: the owner whose values are in registers, and the running minimum over its candidates
     int cur = o;
@@ -127,11 +134,12 @@ DEV int coop_search(int cnt, int off, float scale, const uint16_t *neigh, int ne
         for (int r = 0; r < 8; ++r) {
             if (r < rend) {
                 if (j >= ocnt && r0 + r < np) {         // the owner's list ends: on to the next lane with a list
-                    o = oi.w >> 16;
-                    oi = ws.info[o];
-                    ocnt = oi.w & 0xffff;
-                    ol = oi.x + 1;
+                    o = onext;
+                    ol = nx.x + 1;
+                    ocnt = nx.y & 0xffff;
+                    onext = nx.y >> 16;
                     j = 0;
+                    nx = ws.nxt[o];                     // (needed at the next change of owner only)
                 }
                 const int jc = j < ocnt ? j : ocnt - 1;
                 own_j[r] = o | (jc << 6);
