@@ -34,7 +34,7 @@ struct CoopWS {
 static constexpr int COOP_WS_BYTES = (int)sizeof(CoopWS);
 
 // write this lane's values for the search: n values and n weights
-template <int NV> DEV void coop_stage(CoopWS &ws, const float *xv, const float *wv) {
+template <int NV, class W> DEV void coop_stage(W &ws, const float *xv, const float *wv) {
     float4 *s = (float4 *)ws.stage[lane_id()];
 #pragma unroll
     for (int i = 0; i < NV / 4; ++i) {
@@ -44,7 +44,7 @@ template <int NV> DEV void coop_stage(CoopWS &ws, const float *xv, const float *
 }
 
 // an owner's staged values into registers
-DEV void coop_fetch(const CoopWS &ws, int owner, float (&st)[16]) {
+template <class W> DEV void coop_fetch(const W &ws, int owner, float (&st)[16]) {
     const float4 *sp = (const float4 *)ws.stage[owner];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -174,4 +174,145 @@ DEV int coop_search(int cnt, int off, float scale, const uint16_t *neigh, int ne
     const unsigned long long k = ws.key[lane];
     if ((unsigned)(k >> 32) >= 0x7f7fffffu) return -1;  // min distance >= FLT_MAX (or NaN): nothing accepted
     return (int)(k & 0xfffu);
+}
+
+// ------------------------------------------------------------------ several lists a lane
+// The same search over M lists a lane (M = 2 or 4; the lane's values, staged once, and a scale per list): the wave's
+// 64*M lists are concatenated lane by lane, list by list (list e = lane*M + m), and dealt out as above. One call then
+// covers M searches of every lane, so the set-up and the last, partly filled round are paid once for the M.
+// The stage sits at the start, as in CoopWS, so both searches can share one workspace and its staged values.
+template <int M> struct CoopWSM {
+    static_assert(M == 2 || M == 4, "lists a lane: 2 or 4");
+    float stage[64][16];            // a lane's values: 8 x's then 8 weights
+    int2 ent[64 * M];               // list e: offset | length << 21, the next list with candidates | e << 8
+    float esc[64 * M];              // list e: its scale
+    unsigned long long key[64 * M]; // list e: min of (distance bits << 32 | list position << 12 | grid index)
+    int mark[64];                   // walker lane: the list of its first position | position in that list << 8
+};
+template <int M> constexpr int coop_wsm_bytes() { return (int)sizeof(CoopWSM<M>); }
+
+// cnt[m]: the length of the lane's list m (0: no search), off[m]: its offset in neigh (packed as off | cnt << 21 must
+// fit 31 bits: off < 2^21, cnt < 2^10), scale[m]: its scale. gi[m]: the winner (-1: none accepted; -2: cnt[m] == 0).
+template <int M, class Eval>
+DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&scale)[M], const uint16_t *neigh,
+                       int neigh_len, CoopWSM<M> &ws, const Eval &ev, int (&gi)[M]) {
+    constexpr int LM = M == 4 ? 2 : 1;
+    const __amdgpu_buffer_rsrc_t nrs = __builtin_amdgcn_make_buffer_rsrc((void *)neigh, 0, neigh_len * 2, 0x00020000);
+    const int lane = lane_id();
+    int tot = 0;
+#pragma unroll
+    for (int m = 0; m < M; ++m) tot += cnt[m];
+    const int incl = wave_incl_scan(tot);
+    const int total = __builtin_amdgcn_readlane(incl, 63);
+#pragma unroll
+    for (int m = 0; m < M; ++m) gi[m] = -2;
+    if (total == 0) return;                             // wave-uniform
+    const unsigned long long has = __ballot(tot > 0);
+    // the lane's first and last lists with candidates; the first list of the next lane with candidates
+    int first = -1, last = -1;
+#pragma unroll
+    for (int m = M - 1; m >= 0; --m)
+        if (cnt[m] > 0) first = lane * M + m;
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+        if (cnt[m] > 0) last = lane * M + m;
+    const unsigned long long after = has & ~((2ull << lane) - 1);
+    const int nfirst = __shfl(first, after ? __ffsll((long long)after) - 1 : lane);
+    // the wave's last list (read here, in wave-uniform control flow: a lane read inside a branch may not have been
+    // computed there)
+    const int wlast = __builtin_amdgcn_readlane(last, 63 - __clzll(has));
+    {
+        int carry = after ? nfirst : -1;                // (the wave's last list links to itself)
+#pragma unroll
+        for (int m = M - 1; m >= 0; --m) {
+            const int e = lane * M + m;
+            ws.ent[e] = make_int2(off[m] | (cnt[m] << 21), (carry < 0 ? e : carry) | (e << 8));
+            ws.esc[e] = scale[m];
+            ws.key[e] = ~0ull;
+            if (cnt[m] > 0) carry = e;
+        }
+    }
+    const int R = (total + 63) >> 6;                    // positions a lane
+    {
+        int start = incl - tot;                         // the list's first position
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            if (cnt[m] > 0) {                           // walkers L with start <= L*R < start + cnt begin in list m
+                const int lf = div_small(start + R - 1, R);
+                const int ll = div_small(start + cnt[m] - 1, R);
+                for (int L = lf; L <= ll && L < 64; ++L) ws.mark[L] = (lane * M + m) | ((L * R - start) << 8);
+            }
+            start += cnt[m];
+        }
+    }
+    wave_sync();
+    const int p0 = lane * R;
+    const int np = total - p0 < R ? (total - p0 > 0 ? total - p0 : 0) : R;
+    int o, j;
+    if (np) {
+        const int mk = ws.mark[lane];
+        o = mk & 255;
+        j = mk >> 8;
+    } else {                                            // (idle lane: repeats the wave's last list's first candidate)
+        o = wlast;
+        j = 0;
+    }
+    const int2 oe = ws.ent[o];
+    int ocnt = oe.x >> 21;
+    int ol = (oe.x & ((1 << 21) - 1)) + 1;              // the list's first entry
+    int2 nx = ws.ent[oe.y & 255];                       // the entry of the list after it (read ahead)
+    int cur = o;
+    float st[16], sc = ws.esc[o];
+    unsigned long long kmin = ~0ull;
+    coop_fetch(ws, o >> LM, st);
+    for (int r0 = 0; r0 < R; r0 += 8) {
+        const int rend = R - r0 < 8 ? R - r0 : 8;
+        int own_j[8], idx[8];           // list | list position << 8; the candidate's grid index
+        uint64_t pt[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            if (r < rend) {
+                if (j >= ocnt && r0 + r < np) {
+                    o = nx.y >> 8;
+                    ol = (nx.x & ((1 << 21) - 1)) + 1;
+                    ocnt = nx.x >> 21;
+                    j = 0;
+                    nx = ws.ent[nx.y & 255];
+                }
+                const int jc = j < ocnt ? j : ocnt - 1;
+                own_j[r] = o | (jc << 8);
+                idx[r] = __builtin_amdgcn_raw_buffer_load_b16(nrs, (ol + jc) * 2, 0, 0);
+                ++j;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+            if (r < rend) pt[r] = ev.point(idx[r]);
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            if (r < rend) {
+                const int e = own_j[r] & 255;
+                if (e != cur) {
+                    atomicMin(&ws.key[cur], kmin);
+                    if ((e ^ cur) >> LM) coop_fetch(ws, e >> LM, st);
+                    cur = e;
+                    kmin = ~0ull;
+                    sc = ws.esc[e];
+                }
+                const float d2 = ev(st, sc, pt[r]);
+                const unsigned long long key = ((unsigned long long)__float_as_uint(d2) << 32) |
+                                               (((unsigned)(own_j[r] >> 8) << 12) | (unsigned)idx[r]);
+                kmin = key < kmin ? key : kmin;
+            }
+        }
+    }
+    atomicMin(&ws.key[cur], kmin);
+    wave_sync();
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        if (cnt[m] > 0) {
+            const unsigned long long k = ws.key[lane * M + m];
+            gi[m] = (unsigned)(k >> 32) >= 0x7f7fffffu ? -1 : (int)(k & 0xfffu);
+        }
+    }
 }

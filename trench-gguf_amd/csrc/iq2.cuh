@@ -156,14 +156,18 @@ DEV void sums_q8(const float *w, const float *xv, uint64_t pt, float &sumqx, flo
 // block: d qs[32] u16 (66 bytes); lane g = 32-weight sub-block g; q2[2g] at 2+8g, q2[2g+1] at 6+8g
 struct KIQ2XXS : Iq8Tab<256> {
     static constexpr int BS = QK, G = 8, N = 32, BB = 66, NTRIAL = 13;
-    // per-wave LDS: the search workspace, then every trial's 4 grid indices (a u32 per trial and lane)
-    static constexpr int WS = COOP_WS_BYTES + NTRIAL * 64 * 4;
+    static constexpr int MT = 4;        // trials searched by one wave-wide call
+    // per-wave LDS: the search workspace (the single-list and the MT-list searches share it and its staged values),
+    // then every trial's 4 grid indices (a u32 per trial and lane)
+    static constexpr int WSB = coop_wsm_bytes<MT>() > COOP_WS_BYTES ? coop_wsm_bytes<MT>() : COOP_WS_BYTES;
+    static constexpr int WS = WSB + NTRIAL * 64 * 4;
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
                           const QParams &p) {
         const uint64_t *grid = Iq8Tab<256>::grid(lds);
         const int32_t *map3 = Iq8Tab<256>::map3(lds);
         CoopWS &ws = *(CoopWS *)wave_ws<KIQ2XXS>(img);
-        uint32_t *gtab = (uint32_t *)(wave_ws<KIQ2XXS>(img) + COOP_WS_BYTES) + lane_id();   // [trial * 64]
+        CoopWSM<MT> &wsm = *(CoopWSM<MT> *)wave_ws<KIQ2XXS>(img);
+        uint32_t *gtab = (uint32_t *)(wave_ws<KIQ2XXS>(img) + WSB) + lane_id();   // [trial * 64]
         float weight[N], xval[N];
         uint32_t bsg = 0;       // the 4 groups' 7-bit sign fields
         {
@@ -206,11 +210,35 @@ struct KIQ2XXS : Iq8Tab<256> {
             for (int i = 0; i < 8; ++i) waux[i] = sqrtf(weight[i]);
             coop_stage<8>(ws, xk, waux);
 #pragma unroll 1
-            for (int t = 0; t < NTRIAL; ++t) {
-                const float id = idv[t], this_scale = tsv[t];
-                bool og;
-                const int gi = group_point_s(live, group_key3(xk, id), map3, p, grid, this_scale, ws, og);
-                ((uint8_t *)(gtab + t * 64))[k] = (uint8_t)gi;
+            for (int t0 = 0; t0 < NTRIAL; t0 += MT) {
+                // trials t0 .. t0+MT-1: a key on the grid takes its point, the others search together; a search that
+                // accepts nothing flags the error (the reference traps) and yields 0
+                int mk[MT], cnt[MT], off[MT], gi[MT];
+                float tsc[MT];
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    const int t = t0 + m < NTRIAL ? t0 + m : NTRIAL - 1;
+                    const bool act = live && t0 + m < NTRIAL;
+                    mk[m] = act ? map3[group_key3(xk, idv[t])] : 0;
+                    off[m] = mk[m] < 0 ? m3_off(mk[m]) : 0;
+                    cnt[m] = mk[m] < 0 ? m3_cnt(mk[m]) : 0;
+                    tsc[m] = tsv[t];
+                }
+                coop_search_m<MT>(cnt, off, tsc, p.neigh, p.neigh_len, wsm, EvalIq8{grid}, gi);
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    if (t0 + m < NTRIAL) {
+                        int g = mk[m];
+                        if (g < 0) {
+                            g = gi[m];
+                            if (g < 0) {
+                                flag_err(p);
+                                g = 0;
+                            }
+                        }
+                        ((uint8_t *)(gtab + (t0 + m) * 64))[k] = (uint8_t)g;
+                    }
+                }
             }
             rot8(xval);
             rot8(weight);
