@@ -111,7 +111,7 @@ bool valid_search(int t, const std::vector<uint64_t> &grid, const std::vector<in
         if (off >= NL) return false;
         const int cnt = neigh[off];
         if (cnt < 1 || off + cnt >= NL) return false;
-        if (e8 && (off >= (1 << M3_OFF_BITS) || cnt >= (1 << (31 - M3_OFF_BITS)))) return false;
+        if (e8 && (off + 1 >= (1 << M3_OFF_BITS) || cnt >= (1 << (31 - M3_OFF_BITS)))) return false;
         for (int j = 1; j <= cnt; ++j)
             if (neigh[off + j] >= G) return false;
     }

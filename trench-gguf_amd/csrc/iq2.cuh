@@ -72,6 +72,7 @@ struct EvalIq8 {
 // grid takes that point (og = true), the others search their neighbour lists together (coop_search) with the values
 // the caller staged (coop_stage). Inactive lanes get 0. A search that accepts nothing flags the error (the reference
 // traps) and yields 0.
+template <int CH = 8>
 DEV int group_point_s(bool active, int k3, const int32_t *map3, const QParams &p, const uint64_t *grid, float scale,
                       CoopWS &ws, bool &og) {
     const int m = active ? map3[k3] : 0;
@@ -79,7 +80,7 @@ DEV int group_point_s(bool active, int k3, const int32_t *map3, const QParams &p
     const bool srch = active && m < 0;
     const int off = srch ? m3_off(m) : 0;
     const int cnt = srch ? m3_cnt(m) : 0;
-    const int gi = coop_search(cnt, off, scale, p.neigh, p.neigh_len, ws, EvalIq8{grid});
+    const int gi = coop_search<CH>(cnt, off, scale, p.neigh, p.neigh_len, ws, EvalIq8{grid});
     if (!srch) return active ? m : 0;
     if (gi < 0) {
         flag_err(p);
@@ -89,10 +90,11 @@ DEV int group_point_s(bool active, int k3, const int32_t *map3, const QParams &p
 }
 
 // the same, staging the group's values (x's xv, weights wa) first
+template <int CH = 8>
 DEV int group_point_w(bool active, int k3, const int32_t *map3, const QParams &p, const uint64_t *grid,
                       const float *xv, const float *wa, float scale, CoopWS &ws, bool &og) {
     coop_stage<8>(ws, xv, wa);
-    return group_point_s(active, k3, map3, p, grid, scale, ws, og);
+    return group_point_s<CH>(active, k3, map3, p, grid, scale, ws, og);
 }
 
 // signs of 8 values with even parity: an odd count flips the weight with the least w*x^2 (gpuq/gpuq.hip:272-289)
@@ -308,6 +310,8 @@ struct KIQ2XXS : Iq8Tab<256> {
 // ------------------------------------------------------------------ IQ2_XS / IQ2_S: the 16-weight search
 // (gpuq/gpuq.hip:690-822, 824-969). Returns the sub-block scale; gidx the two grid indices, bsg the two sign bytes;
 // live = false for a skipped (negligible) sub-block.
+// the 16-weight searches' neighbour lists are short (a few rounds a call): chunks of 2 rounds waste the least
+constexpr int CH16 = 2;
 template <bool PARITY, int GRID>
 DEV float iq2_16_search(const float (&x)[16], const float (&qv)[16], float sigma2, float eps, const QParams &p,
                         const uint8_t *lds, CoopWS &ws, int (&gidx)[2], uint32_t (&bsg)[2], bool &live) {
@@ -340,7 +344,7 @@ DEV float iq2_16_search(const float (&x)[16], const float (&qv)[16], float sigma
         float sumqx = 0, sumq2 = 0;
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
-            Pa[k] = group_point_w(live, group_key3(xval + 8 * k, id), map3, p, grid, xval + 8 * k, waux + 8 * k,
+            Pa[k] = group_point_w<CH16>(live, group_key3(xval + 8 * k, id), map3, p, grid, xval + 8 * k, waux + 8 * k,
                                   this_scale, ws, og[k]);
             sums_q8(weight + 8 * k, xval + 8 * k, grid[Pa[k]], sumqx, sumq2);
         }
@@ -362,7 +366,7 @@ DEV float iq2_16_search(const float (&x)[16], const float (&qv)[16], float sigma
         for (int k = 0; k < 2; ++k) {
             const bool act = fin && !on_grid[k];
             bool og;
-            const int gi = group_point_w(act, group_key3(xval + 8 * k, id), map3, p, grid, xval + 8 * k,
+            const int gi = group_point_w<CH16>(act, group_key3(xval + 8 * k, id), map3, p, grid, xval + 8 * k,
                                          waux + 8 * k, scale, ws, og);
             if (act) P[k] = gi;
             sums_q8(weight + 8 * k, xval + 8 * k, grid[P[k] < 0 ? 0 : P[k]], sumqx, sumq2);
