@@ -286,6 +286,26 @@ size_t quantize_host(int src, const void *raw, int type, void *dst, int64_t nmat
     return out_bytes;
 }
 
+// the LDLQ loop's side stream and its events (created once, on the library's device; default priority)
+hipStream_t g_st2 = nullptr;
+hipEvent_t g_ev_start = nullptr, g_ev_solved = nullptr, g_ev_rest = nullptr;
+bool side_stream_ready() {
+    if (g_st2) return true;
+    if (hipStreamCreateWithFlags(&g_st2, hipStreamNonBlocking) != hipSuccess) return false;
+    for (hipEvent_t *e : {&g_ev_start, &g_ev_solved, &g_ev_rest})
+        if (hipEventCreateWithFlags(e, hipEventDisableTiming) != hipSuccess) return false;
+    return true;
+}
+
+// W -= Es . U[c0 .. c0+255][cb .. ce) for every matrix
+bool launch_update(float *W, const double *Es, const double *U, int64_t u_stride, int64_t nmat, int64_t ne1,
+                   int64_t ne0, int64_t c0, int64_t cb, int64_t ce, hipStream_t st) {
+    const dim3 ug((unsigned)((ce - cb + LDLQ_TN - 1) / LDLQ_TN), (unsigned)((ne1 + LDLQ_TM - 1) / LDLQ_TM),
+                  (unsigned)nmat);
+    hipLaunchKernelGGL(k_ldlq_update, ug, dim3(256), 0, st, W, Es, U, u_stride, ne1, ne0, c0, cb, ce);
+    return hipGetLastError() == hipSuccess;
+}
+
 bool ldlq_type(int t) {
     return t == T_IQ2_XXS || t == T_IQ2_XS || t == T_IQ2_S || t == T_IQ3_XXS || t == T_IQ3_S || t == T_IQ1_S ||
            t == T_IQ1_M || t == T_IQ4_XS;
@@ -519,7 +539,17 @@ extern "C" size_t gpuq_ldlq_dev(int type, float *d_wp, const double *d_u, int64_
     const hipStream_t st = (hipStream_t)stream;
     const int64_t bb = (int64_t)gpuq_block_bytes(type), rows = nmat * ne1;
     std::lock_guard<std::mutex> lock(g_mu);
-    if (feedback && nblk > 1 && !g_es.grow((size_t)rows * QK * 8)) return 0;
+    const bool fb = feedback && nblk > 1;
+    // Es of two consecutive blocks (the update of block k's later columns still reads Es(k) while Es(k+1) is solved)
+    if (fb && (!g_es.grow((size_t)2 * rows * QK * 8) || !side_stream_ready())) return 0;
+    // Block k's update is split: the next block's 256 columns on the caller's stream (they gate quantizing block
+    // k+1), the rest on a side stream, where it runs alongside block k+1's quantization and solve. Every column still
+    // receives its updates in block order: the next-block part of update k waits for the side stream's update k-1.
+    if (fb) {
+        if (hipEventRecord(g_ev_start, st) != hipSuccess || hipStreamWaitEvent(g_st2, g_ev_start, 0) != hipSuccess)
+            return 0;
+    }
+    bool rest_pending = false;      // a side-stream update not yet waited for by the caller's stream
     for (int64_t k = 0; k < nblk; ++k) {
         const int64_t c0 = k * QK;
         QParams p = params_for(type, d_wp, d_out, rows, d_qw, ne1, 1, 1);
@@ -530,15 +560,29 @@ extern "C" size_t gpuq_ldlq_dev(int type, float *d_wp, const double *d_u, int64_
         p.out_stride = nblk * bb;
         p.out_off = blk_order[k] * bb;
         if (!dispatch(type, T_F32, p, st)) return 0;
-        if (!feedback || k + 1 >= nblk) continue;
+        if (!fb || k + 1 >= nblk) continue;
+        double *es = (double *)g_es.p + (size_t)(k & 1) * rows * QK;
         if (!launch_solve(type, d_wp, (const uint8_t *)d_out, nblk * bb, blk_order[k] * bb, d_u, u_stride, nmat, ne1,
-                          ne0, c0, (double *)g_es.p, st))
+                          ne0, c0, es, st))
             return 0;
-        const dim3 ug((unsigned)((ne0 - c0 - QK + LDLQ_TN - 1) / LDLQ_TN), (unsigned)((ne1 + LDLQ_TM - 1) / LDLQ_TM),
-                      (unsigned)nmat);
-        hipLaunchKernelGGL(k_ldlq_update, ug, dim3(256), 0, st, d_wp, (const double *)g_es.p, d_u, u_stride, ne1, ne0,
-                           c0);
-        if (hipGetLastError() != hipSuccess) return 0;
+        if (hipEventRecord(g_ev_solved, st) != hipSuccess) return 0;
+        if (rest_pending) {
+            if (hipStreamWaitEvent(st, g_ev_rest, 0) != hipSuccess) return 0;
+            rest_pending = false;
+        }
+        const int64_t cn = c0 + 2 * QK < ne0 ? c0 + 2 * QK : ne0;
+        if (!launch_update(d_wp, es, d_u, u_stride, nmat, ne1, ne0, c0, c0 + QK, cn, st)) return 0;
+        if (cn < ne0) {
+            if (hipStreamWaitEvent(g_st2, g_ev_solved, 0) != hipSuccess ||
+                !launch_update(d_wp, es, d_u, u_stride, nmat, ne1, ne0, c0, cn, ne0, g_st2) ||
+                hipEventRecord(g_ev_rest, g_st2) != hipSuccess)
+                return 0;
+            rest_pending = true;
+        }
+    }
+    if (fb) {       // the caller's stream joins the side stream
+        if (hipEventRecord(g_ev_rest, g_st2) != hipSuccess || hipStreamWaitEvent(st, g_ev_rest, 0) != hipSuccess)
+            return 0;
     }
     return (size_t)(rows * nblk * bb);
 }

@@ -36,7 +36,8 @@ __global__ __launch_bounds__(64) void k_ldlq_solve(const float *__restrict__ W, 
     const double *Um = U + m * u_stride;
     const float *wrow = W + r * ne0 + c0;
     const uint8_t *qb = q + r * q_stride + q_off;
-    double *es = Es + r * QK;
+    const int64_t R = (int64_t)gridDim.y * ne1;            // Es rows (k-major: Es[k * R + r])
+    double *es = Es + r;
     for (int c = 0; c < 8; ++c) {
         float y[32];
         dq_chunk<TYPE>(qb, c, y, grid);
@@ -51,7 +52,7 @@ __global__ __launch_bounds__(64) void k_ldlq_solve(const float *__restrict__ W, 
             acc[4 * t + 3] = (double)(v.w - y[4 * t + 3]);
         }
         for (int i = 0; i < 32 * c; ++i) {
-            const double e = es[i];
+            const double e = es[i * R];
             const double *urow = Um + (c0 + i) * ne0 + c0 + 32 * c;
 #pragma unroll
             for (int t = 0; t < 32; ++t) acc[t] = fma(-e, urow[t], acc[t]);
@@ -60,25 +61,30 @@ __global__ __launch_bounds__(64) void k_ldlq_solve(const float *__restrict__ W, 
         for (int i = 0; i < 32; ++i) {
             const double *urow = Um + (c0 + 32 * c + i) * ne0 + c0 + 32 * c;
             const double v = acc[i] / urow[i];
-            if (live) es[32 * c + i] = v;
+            if (live) es[(32 * c + i) * R] = v;
 #pragma unroll
             for (int t = i + 1; t < 32; ++t) acc[t] = fma(-v, urow[t], acc[t]);
         }
     }
 }
 
-// W[m][row][c] -= (float)(Es[m*ne1+row][:] . U_m[c0 .. c0+255][c]) for c in [c0 + 256, ne0). A workgroup of 4 waves
-// owns a 128 x 128 tile (each wave 64 x 64: 4 x 4 MFMA tiles of 16 x 16); k runs in chunks of 16 staged in LDS
-// (k-major, padded rows) and 4 MFMA k-steps a chunk.
+// W[m][row][c] -= (float)(sum_i Es[c0+i][m*ne1+row] U_m[c0+i][c]) for c in [cb, ce) (later columns than block
+// c0's: cb >= c0 + 256). Es is k-major (Es[k][row], k < 256). A workgroup of 4 waves owns a 128 x 128 tile (each
+// wave 64 x 64: 4 x 4 MFMA tiles of 16 x 16); k runs in chunks of 16 staged in LDS, k-major, two buffers (one barrier
+// a chunk). A loader thread moves k row t/16, elements t%16 + 16j: 16 lanes read 128 contiguous bytes and write 16
+// consecutive LDS doubles; LDS rows are 144 doubles apart (1152 B = 128 mod 256), so the MFMA operand reads (4 k
+// rows x 16 consecutive doubles a wave) and the loader's writes fall in distinct banks.
+#define LDLQ_LDS_ROW 144
 typedef double ldlq_d4 __attribute__((ext_vector_type(4)));
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_ldlq_update(float *__restrict__ W, const double *__restrict__ Es,
-                                                     const double *__restrict__ U, int64_t u_stride, int64_t ne1,
-                                                     int64_t ne0, int64_t c0) {
-    __shared__ __align__(16) double As[LDLQ_BK][LDLQ_TM + 2];
-    __shared__ __align__(16) double Bs[LDLQ_BK][LDLQ_TN + 2];
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_ldlq_update(
+    float *__restrict__ W, const double *__restrict__ Es, const double *__restrict__ U, int64_t u_stride, int64_t ne1,
+    int64_t ne0, int64_t c0, int64_t cb, int64_t ce) {
+    __shared__ __align__(16) double As[2][LDLQ_BK][LDLQ_LDS_ROW];
+    __shared__ __align__(16) double Bs[2][LDLQ_BK][LDLQ_LDS_ROW];
     const int64_t m = blockIdx.z;
+    const int64_t R = (int64_t)gridDim.z * ne1;
     const int64_t row0 = (int64_t)blockIdx.y * LDLQ_TM;
-    const int64_t col0 = c0 + QK + (int64_t)blockIdx.x * LDLQ_TN;
+    const int64_t col0 = cb + (int64_t)blockIdx.x * LDLQ_TN;
     const double *Um = U + m * u_stride;
     const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
     const int wr0 = (wave >> 1) * 64, wc0 = (wave & 1) * 64;   // the wave's 64 x 64 sub-tile
@@ -87,46 +93,86 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     for (int a = 0; a < 4; ++a)
 #pragma unroll
         for (int b = 0; b < 4; ++b) acc[a][b] = ldlq_d4{0.0, 0.0, 0.0, 0.0};
-    // loader roles (E = BK/2 values a thread a tile): A: row tid/2, k half (tid%2)*E; B: k row tid/(128/E), columns
-    // E*(tid%(128/E))
-    constexpr int E = LDLQ_BK / 2, BPR = LDLQ_TN / E;
-    const int ar = tid / 2, ak = (tid % 2) * E;
-    const int bk = tid / BPR, bc = E * (tid % BPR);
-    const bool a_ok = row0 + ar < ne1;
-    const double *arow = Es + (m * ne1 + (a_ok ? row0 + ar : 0)) * QK;
-    // the next chunk's global reads are issued before the current chunk's MFMAs, so they overlap
-    double av[E], bv[E];
+    static_assert(LDLQ_BK * 16 == 256 && LDLQ_TM == 128 && LDLQ_TN == 128, "loader: 16 k rows x 16 lanes, 8 a thread");
+    const int lk = tid >> 4, le = tid & 15;
+    const double *abase = Es + m * ne1 + row0 + le;          // + k * R + 16 j
+    const double *bbase = Um + col0 + le;                     // + (c0 + k) * ne0 + 16 j
+    double av[8], bv[8];
     auto load = [&](int k0) {
+        const double *ap = abase + (int64_t)(k0 + lk) * R;
+        const double *bp = bbase + (c0 + k0 + lk) * ne0;
 #pragma unroll
-        for (int j = 0; j < E; ++j) av[j] = a_ok ? arow[k0 + ak + j] : 0.0;
-        const double *brow = Um + (c0 + k0 + bk) * ne0;
+        for (int j = 0; j < 8; ++j) av[j] = row0 + le + 16 * j < ne1 ? ap[16 * j] : 0.0;
 #pragma unroll
-        for (int j = 0; j < E; ++j) bv[j] = col0 + bc + j < ne0 ? brow[col0 + bc + j] : 0.0;
+        for (int j = 0; j < 8; ++j) bv[j] = col0 + le + 16 * j < ce ? bp[16 * j] : 0.0;
+    };
+    auto stash = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) As[buf][lk][le + 16 * j] = av[j];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) Bs[buf][lk][le + 16 * j] = bv[j];
     };
     load(0);
+    stash(0);
+    __syncthreads();
+    int buf = 0;
     for (int k0 = 0; k0 < QK; k0 += LDLQ_BK) {
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < E; ++j) As[ak + j][ar] = av[j];
-#pragma unroll
-        for (int j = 0; j < E; ++j) Bs[bk][bc + j] = bv[j];
-        __syncthreads();
-        if (k0 + LDLQ_BK < QK) load(k0 + LDLQ_BK);
+        const bool more = k0 + LDLQ_BK < QK;
+        if (more) load(k0 + LDLQ_BK);       // the next chunk's global reads overlap this chunk's MFMAs
 #pragma unroll
         for (int ks = 0; ks < LDLQ_BK; ks += 4) {
             const int kk = ks + lane / 16;
             double a[4], b[4];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                a[t] = As[kk][wr0 + 16 * t + lane % 16];
-                b[t] = Bs[kk][wc0 + 16 * t + lane % 16];
+                a[t] = As[buf][kk][wr0 + 16 * t + lane % 16];
+                b[t] = Bs[buf][kk][wc0 + 16 * t + lane % 16];
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[i], b[j], acc[i][j], 0, 0, 0);
         }
+        if (more) stash(buf ^ 1);           // (the other buffer was last read before the previous barrier)
+        __syncthreads();
+        buf ^= 1;
     }
+    // epilogue: every W value of the wave's sub-tile is read before the first store (a store between the reads
+    // would make each read wait for the one before it); a tile inside the matrix (the usual case) runs unguarded, so
+    // the stores need no per-element branches (and their waits no conservative counts)
+    const bool full = row0 + LDLQ_TM <= ne1 && col0 + LDLQ_TN <= ce;
+    float wv[4][4][4];
+    if (full) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float *wr = W + (m * ne1 + row0 + wr0 + 16 * i + 4 * e + lane / 16) * ne0 + col0 + wc0 + lane % 16;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) wv[i][e][j] = wr[16 * j];
+            }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float *wr = W + (m * ne1 + row0 + wr0 + 16 * i + 4 * e + lane / 16) * ne0 + col0 + wc0 + lane % 16;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) wr[16 * j] = wv[i][e][j] - (float)acc[i][j][e];
+            }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int64_t row = row0 + wr0 + 16 * i + 4 * e + lane / 16;
+            const float *wr = W + (m * ne1 + (row < ne1 ? row : 0)) * ne0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int64_t col = col0 + wc0 + 16 * j + lane % 16;
+                wv[i][e][j] = row < ne1 && col < ce ? wr[col] : 0.f;
+            }
+        }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -137,7 +183,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int64_t col = col0 + wc0 + 16 * j + lane % 16;
-                if (col < ne0) wr[col] = wr[col] - (float)acc[i][j][e];
+                if (col < ce) wr[col] = wv[i][e][j] - (float)acc[i][j][e];
             }
         }
 }
