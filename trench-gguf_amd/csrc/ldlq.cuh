@@ -3,9 +3,9 @@
 // For column block k (256 permuted columns, c0 = 256k) of nmat matrices of ne1 rows:
 //   1. the quantizer runs on the strided view of block k of every row (frame.cuh) and writes each row's block
 //      into its output slot;
-//   2. k_ldlq_solve, one lane a row: E = blk - to_float(block bytes) in f32, then Es = E U_BB^-1 by forward
-//      substitution in f64: Es[j] = (E[j] - sum_{i<j} Es[i] U[c0+i][c0+j]) / U[c0+j][c0+j], each sum a fused
-//      multiply-add chain over i in ascending order;
+//   2. k_ldlq_solve: E = blk - to_float(block bytes) in f32, then Es = E U_BB^-1 by forward substitution in f64:
+//      Es[j] = (E[j] - sum_{i<j} Es[i] U[c0+i][c0+j]) / U[c0+j][c0+j], each sum a fused multiply-add chain over i in
+//      ascending order (the part over earlier 32-column chunks on the matrix cores);
 //   3. k_ldlq_update, an f64 GEMM on the matrix cores: W[r][c] -= (float)(sum_{i<256} Es[r][i] U[c0+i][c]) for the
 //      later columns c, each output a fused multiply-add chain over i in ascending order from 0.0.
 // The reference leaves the order of those sums to LAPACK / BLAS (numpy's LU solve, torch's solve_triangular and
@@ -15,6 +15,7 @@
 // included), so a chain of them over k = 0, 4, ..., 252 is exactly the ascending fma chain; its output layout is
 // lane l, element e -> row 4e + l/16, column l%16.
 #pragma once
+#include "frame.cuh"
 #include "dequant.cuh"
 
 #ifndef LDLQ_BK
@@ -23,48 +24,105 @@
 #define LDLQ_TM 128           // update tile rows
 #define LDLQ_TN 128           // update tile columns
 
-// one wave = 64 rows of one matrix (blockIdx.y), so U's addresses are wave-uniform (scalar loads)
+typedef double ldlq_d4 __attribute__((ext_vector_type(4)));
+
+// One wave = 64 rows of one matrix (blockIdx.y); the block's 256 columns in chunks of 32. Chunk c:
+//   E = blk - to_float(bytes) (f32, then f64), one lane a row, into LDS;
+//   E -= Es[:, 0 .. 32c) U[0 .. 32c, chunk] on the f64 matrix cores (each output an fma chain over ascending k,
+//   started from E: the serial loop's order), with Es read back (k-major) from the earlier chunks' stores;
+//   the 32 x 32 triangle by forward substitution, one lane a row, U's diagonal block broadcast from LDS.
 template <int TYPE>
-__global__ __launch_bounds__(64) void k_ldlq_solve(const float *__restrict__ W, const uint8_t *__restrict__ q,
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_ldlq_solve(const float *__restrict__ W, const uint8_t *__restrict__ q,
                                                    int64_t q_stride, int64_t q_off, const double *__restrict__ U,
                                                    int64_t u_stride, int64_t ne1, int64_t ne0, int64_t c0,
                                                    double *__restrict__ Es, const uint64_t *__restrict__ grid) {
+    __shared__ double T[64][33];            // the chunk's 64 rows x 32 columns (33: a row per lane hits distinct banks)
+    __shared__ double Ud[32][32];           // U's diagonal block of the chunk
     const int64_t m = blockIdx.y;
-    const int64_t row = (int64_t)blockIdx.x * 64 + threadIdx.x;
+    const int lane = lane_id();
+    const int64_t row0 = (int64_t)blockIdx.x * 64, row = row0 + lane;
     const bool live = row < ne1;
     const int64_t r = m * ne1 + (live ? row : ne1 - 1);
+    const int64_t R = (int64_t)gridDim.y * ne1;            // Es rows (k-major: Es[k * R + r])
     const double *Um = U + m * u_stride;
     const float *wrow = W + r * ne0 + c0;
     const uint8_t *qb = q + r * q_stride + q_off;
-    const int64_t R = (int64_t)gridDim.y * ne1;            // Es rows (k-major: Es[k * R + r])
-    double *es = Es + r;
+    // MFMA operand rows of this lane (rows past the matrix read row ne1 - 1: their results are not stored)
+    int64_t arow[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const int64_t rr = row0 + 16 * t + lane % 16;
+        arow[t] = m * ne1 + (rr < ne1 ? rr : ne1 - 1);
+    }
     for (int c = 0; c < 8; ++c) {
-        float y[32];
-        dq_chunk<TYPE>(qb, c, y, grid);
-        double acc[32];
-        const float4 *wp = (const float4 *)(wrow + 32 * c);
+        const int64_t cc = c0 + 32 * c;                     // the chunk's first column
+        {
+            float y[32];
+            dq_chunk<TYPE>(qb, c, y, grid);
+            const float4 *wp = (const float4 *)(wrow + 32 * c);
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const float4 v = wp[t];
-            acc[4 * t + 0] = (double)(v.x - y[4 * t + 0]);
-            acc[4 * t + 1] = (double)(v.y - y[4 * t + 1]);
-            acc[4 * t + 2] = (double)(v.z - y[4 * t + 2]);
-            acc[4 * t + 3] = (double)(v.w - y[4 * t + 3]);
+            for (int t = 0; t < 8; ++t) {
+                const float4 v = wp[t];
+                T[lane][4 * t + 0] = (double)(v.x - y[4 * t + 0]);
+                T[lane][4 * t + 1] = (double)(v.y - y[4 * t + 1]);
+                T[lane][4 * t + 2] = (double)(v.z - y[4 * t + 2]);
+                T[lane][4 * t + 3] = (double)(v.w - y[4 * t + 3]);
+            }
         }
-        for (int i = 0; i < 32 * c; ++i) {
-            const double e = es[i * R];
-            const double *urow = Um + (c0 + i) * ne0 + c0 + 32 * c;
+        {
+            const double *up = Um + (cc + lane / 32) * ne0 + cc + lane % 32;
 #pragma unroll
-            for (int t = 0; t < 32; ++t) acc[t] = fma(-e, urow[t], acc[t]);
+            for (int i = 0; i < 16; ++i, up += 2 * ne0) Ud[lane / 32 + 2 * i][lane % 32] = *up;
         }
+        wave_sync();
+        if (c > 0) {
+            ldlq_d4 acc[4][2];
+#pragma unroll
+            for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+                for (int tj = 0; tj < 2; ++tj)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[ti][tj][e] = T[16 * ti + 4 * e + lane / 16][16 * tj + lane % 16];
+            for (int k0 = 0; k0 < 32 * c; k0 += 4) {
+                const int k = k0 + lane / 16;
+                double a[4], b[2];
+#pragma unroll
+                for (int ti = 0; ti < 4; ++ti) a[ti] = -Es[k * R + arow[ti]];
+#pragma unroll
+                for (int tj = 0; tj < 2; ++tj) b[tj] = Um[(c0 + k) * ne0 + cc + 16 * tj + lane % 16];
+#pragma unroll
+                for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+                    for (int tj = 0; tj < 2; ++tj)
+                        acc[ti][tj] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[ti], b[tj], acc[ti][tj], 0, 0, 0);
+            }
+#pragma unroll
+            for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+                for (int tj = 0; tj < 2; ++tj)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) T[16 * ti + 4 * e + lane / 16][16 * tj + lane % 16] = acc[ti][tj][e];
+            wave_sync();
+        }
+        double x[32];
+#pragma unroll
+        for (int t = 0; t < 32; ++t) x[t] = T[lane][t];
+        // (branch-free, the results stored after: a store inside would split the unrolled rows into blocks whose
+        // reordering keeps many of U's values live at once)
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
-            const double *urow = Um + (c0 + 32 * c + i) * ne0 + c0 + 32 * c;
-            const double v = acc[i] / urow[i];
-            if (live) es[(32 * c + i) * R] = v;
+            x[i] = x[i] / Ud[i][i];
 #pragma unroll
-            for (int t = i + 1; t < 32; ++t) acc[t] = fma(-v, urow[t], acc[t]);
+            for (int t = i + 1; t < 32; ++t) x[t] = fma(-x[i], Ud[i][t], x[t]);
         }
+        if (live) {
+            double *ep = Es + (int64_t)(32 * c) * R + r;
+#pragma unroll
+            for (int i = 0; i < 32; ++i, ep += R) *ep = x[i];
+        }
+        // this chunk's Es (stored by other lanes) is read back as MFMA operands by the later chunks
+        __threadfence_block();
+        wave_sync();
     }
 }
 
@@ -75,7 +133,6 @@ __global__ __launch_bounds__(64) void k_ldlq_solve(const float *__restrict__ W, 
 // consecutive LDS doubles; LDS rows are 144 doubles apart (1152 B = 128 mod 256), so the MFMA operand reads (4 k
 // rows x 16 consecutive doubles a wave) and the loader's writes fall in distinct banks.
 #define LDLQ_LDS_ROW 144
-typedef double ldlq_d4 __attribute__((ext_vector_type(4)));
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_ldlq_update(
     float *__restrict__ W, const double *__restrict__ Es, const double *__restrict__ U, int64_t u_stride, int64_t ne1,
     int64_t ne0, int64_t c0, int64_t cb, int64_t ce) {
