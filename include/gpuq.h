@@ -83,7 +83,8 @@ size_t gpuq_requantize_dev(int src_type, const void *d_raw, int type, void *d_ds
  * permuted column order (updated in place), d_u [ne0][ne0] f64 row-major upper factor of the permuted inverse
  * Hessian, d_qw [nmat][ne0] f32 importances in permuted order, blk_order (host) the output slot of each permuted
  * 256-column block, d_out [nmat][ne1][ne0/256 blocks]. The f64 solve and update use fixed-order FMA chains (the CPU
- * oracle computes the same ones). Types: the i-quants with a dequantizer grid and IQ4_XS. Asynchronous. */
+ * oracle computes the same ones). Types: the i-quants with a dequantizer grid and IQ4_XS. Asynchronous on `stream`
+ * (part of each update runs on an internal stream that is joined back into `stream` before the call returns). */
 size_t gpuq_ldlq_dev(int type, float *d_wp, const double *d_u, int64_t u_stride, const float *d_qw, int64_t nmat,
                      int64_t ne1, int64_t ne0, const int64_t *blk_order, int feedback, void *d_out, void *stream);
 
