@@ -153,14 +153,14 @@ struct KIQ1S : Iq8Tab<2048> {
                     const float s2x = i2 < N ? sumx[i2 & (N - 1)] : totx, s2w = i2 < N ? sumw[i2 & (N - 1)] : totw;
                     float sumqx = a_x * xp0 + (s2x - s1x) * xp1 + (totx - s2x) * xp2;
                     float sumq2 = a_w * xp0 * xp0 + (s2w - s1w) * xp1 * xp1 + (totw - s2w) * xp2 * xp2;
-                    if (sumq2 > 0 && sumqx * sumqx > best_score * sumq2) {
+                    if ((sumq2 > 0) & (sumqx * sumqx > best_score * sumq2)) {    // (one branch, both tests)
                         scale = sumqx / sumq2;
                         best_score = scale * sumqx;
                         besti1 = i1; besti2 = i2; best_shift = 1;
                     }
                     sumqx = a_x * xm0 + (s2x - s1x) * xm1 + (totx - s2x) * xm2;
                     sumq2 = a_w * xm0 * xm0 + (s2w - s1w) * xm1 * xm1 + (totw - s2w) * xm2 * xm2;
-                    if (sumq2 > 0 && sumqx * sumqx > best_score * sumq2) {
+                    if ((sumq2 > 0) & (sumqx * sumqx > best_score * sumq2)) {
                         scale = sumqx / sumq2;
                         best_score = scale * sumqx;
                         besti1 = i1; besti2 = i2; best_shift = -1;
@@ -287,9 +287,13 @@ struct KIQ1M : Iq8Tab<2048> {
             float best_score = -FLT_MAX;
             scale = mx;
             int besti1 = -1, besti2 = -1, bk = -1;
+            // i1 rolled (its prefix values read once an iteration), i2 unrolled with a uniform skip below i1: every
+            // prefix read in the inner body is a fixed register
             for (int i1 = 0; i1 <= N; ++i1) {
                 const float a0x = px0[i1], a1x = px1[i1], a0w = pw0[i1], a1w = pw1[i1];
-                for (int i2 = i1; i2 <= N; ++i2) {
+#pragma unroll
+                for (int i2 = 0; i2 <= N; ++i2) {
+                    if (i2 < i1) continue;
                     float qx_p[2], qx_m[2], q2_p[2], q2_m[2];
                     {
                         const float sx = a0x + px0[i2];
@@ -316,7 +320,8 @@ struct KIQ1M : Iq8Tab<2048> {
                     sumq2[3] = q2_m[0] + q2_m[1];
 #pragma unroll
                     for (int k = 0; k < 4; ++k) {
-                        if (sumq2[k] > 0 && sumqx[k] * sumqx[k] > best_score * sumq2[k]) {
+                        // (both tests evaluated: one branch instead of two nested ones; the second has no effects)
+                        if ((sumq2[k] > 0) & (sumqx[k] * sumqx[k] > best_score * sumq2[k])) {
                             scale = sumqx[k] / sumq2[k];
                             best_score = scale * sumqx[k];
                             besti1 = i1; besti2 = i2; bk = k;
