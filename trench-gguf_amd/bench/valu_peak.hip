@@ -1,8 +1,9 @@
 // trench-gguf_amd/bench/valu_peak.hip - the VALU throughput the roofline is priced against.
 //
 // Every wave64 of 2048 workgroups x 4 waves runs 8 independent chains of one non-packed 32-bit VALU instruction
-// (fp32 add, mul, fma; int add) for 4096 x 8 iterations; the rate is 64 lane-instructions per wave instruction over
-// the event-timed kernel. The search kernels' algorithmic op counts are priced against the fp32 rate.
+// (fp32 add, mul, fma; the integer step (b ^ it) + u, which compiles to one v_xad_u32) for 4096 x 8 iterations; the
+// rate is 64 lane-instructions per wave instruction over the event-timed kernel. The search kernels' algorithmic op
+// counts are priced against the fp32 rate.
 #include <hip/hip_runtime.h>
 #include <cstdio>
 
@@ -38,7 +39,7 @@ int main() {
     if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return 1;
     const int wgs = 256 * 8;
     const double lane_instr = (double)wgs * 256 * N_IT * 64;
-    const char *name[4] = {"v_add_f32", "v_mul_f32", "v_xor+v_add_u32", "v_fma_f32"};
+    const char *name[4] = {"v_add_f32", "v_mul_f32", "v_xad_u32", "v_fma_f32"};
     for (int rep = 0; rep < 2; ++rep) {
         for (int op = 0; op < 4; ++op) {
             if (hipEventRecord(e0) != hipSuccess) return 1;
@@ -49,7 +50,7 @@ int main() {
             if (hipEventRecord(e1) != hipSuccess || hipEventSynchronize(e1) != hipSuccess) return 1;
             float ms = 0;
             if (hipEventElapsedTime(&ms, e0, e1) != hipSuccess) return 1;
-            const double per = op == 2 ? 2.0 : 1.0;   // (xor and add: two instructions a step)
+            const double per = 1.0;   // one instruction a step (the int step (b ^ it) + u compiles to one v_xad_u32)
             if (rep) printf("%-16s %8.3f ms  %7.2f T lane-instructions/s\n", name[op], ms,
                             per * lane_instr / (ms * 1e-3) / 1e12);
         }
