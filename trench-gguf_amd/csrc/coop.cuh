@@ -23,22 +23,29 @@
 #pragma once
 #include "frame.cuh"
 
-// per-wave LDS workspace of the search with M lists a lane (list e = lane*M + m)
-template <int M> struct CoopWSM {
+// per-wave LDS workspace of the search with M lists a lane (list e = lane*M + m). The owner values are staged a
+// lane (PL = false: the lane's M lists search for one group) or a list (PL = true: M groups of the lane), SW floats
+// each: NV x's then NV weights (SW = 2 NV).
+template <int M, int SW = 16, bool PL = false> struct CoopWSM {
     static_assert(M == 1 || M == 2 || M == 4, "lists a lane: 1, 2 or 4");
-    float stage[64][16];            // a lane's values: 8 (or 4) x's then 8 (or 4) weights
+    static_assert(SW == 8 || SW == 16, "staged values: 4 or 8 x's and weights");
+    static constexpr int sw = SW;
+    static constexpr bool per_list = PL;
+    float stage[PL ? 64 * M : 64][SW];
     int2 ent[64 * M];               // list e: first point's offset | length << 21, next list with candidates | e << 8
     float esc[64 * M];              // list e: its scale
     unsigned long long key[64 * M]; // list e: min of (distance bits << 32 | list position << 12 | grid index)
     int mark[64];                   // walker lane: the list of its first position | position in that list << 8
 };
-template <int M> constexpr int coop_wsm_bytes() { return (int)sizeof(CoopWSM<M>); }
+template <int M, int SW = 16, bool PL = false> constexpr int coop_wsm_bytes() { return (int)sizeof(CoopWSM<M, SW, PL>); }
 using CoopWS = CoopWSM<1>;
 static constexpr int COOP_WS_BYTES = (int)sizeof(CoopWS);
 
-// write this lane's values for the search: n values and n weights
-template <int NV, class W> DEV void coop_stage(W &ws, const float *xv, const float *wv) {
-    float4 *s = (float4 *)ws.stage[lane_id()];
+// write this lane's values for the search: n values and n weights (slot: the lane, or with per-list staging the
+// lane's list lane*M + m)
+template <int NV, class W> DEV void coop_stage(W &ws, const float *xv, const float *wv, int slot = -1) {
+    static_assert(2 * NV <= W::sw, "staged row too small");
+    float4 *s = (float4 *)ws.stage[slot < 0 ? lane_id() : slot];
 #pragma unroll
     for (int i = 0; i < NV / 4; ++i) {
         s[i] = make_float4(xv[4 * i], xv[4 * i + 1], xv[4 * i + 2], xv[4 * i + 3]);
@@ -50,7 +57,7 @@ template <int NV, class W> DEV void coop_stage(W &ws, const float *xv, const flo
 template <class W> DEV void coop_fetch(const W &ws, int owner, float (&st)[16]) {
     const float4 *sp = (const float4 *)ws.stage[owner];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < W::sw / 4; ++i) {
         const float4 v = sp[i];
         st[4 * i] = v.x; st[4 * i + 1] = v.y; st[4 * i + 2] = v.z; st[4 * i + 3] = v.w;
     }
@@ -92,10 +99,10 @@ DEV int wave_incl_scan(int v) {
 // to itself), so every slot holds a real candidate and needs no check: re-evaluating a candidate changes no minimum.
 // Along a walker's run a list's positions come in increasing order, so a strictly smaller distance alone keeps the
 // first of equal ones; the (distance, position) minimum across walkers is taken once per list visited.
-template <int M, int CH = 8, class Eval>
+template <int M, int CH = 8, class Eval, int SW, bool PL>
 DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&scale)[M], const uint16_t *neigh,
-                       int neigh_len, CoopWSM<M> &ws, const Eval &ev, int (&gi)[M]) {
-    constexpr int LM = M == 4 ? 2 : M == 2 ? 1 : 0;
+                       int neigh_len, CoopWSM<M, SW, PL> &ws, const Eval &ev, int (&gi)[M]) {
+    constexpr int LM = PL ? 0 : (M == 4 ? 2 : M == 2 ? 1 : 0);    // list -> staged row: e >> LM
     constexpr int OFF_MASK = (1 << 21) - 1;
     // the lists through a buffer resource: 32-bit offsets, and reads past the table return 0 instead of faulting
     const __amdgpu_buffer_rsrc_t nrs = __builtin_amdgcn_make_buffer_rsrc((void *)neigh, 0, neigh_len * 2, 0x00020000);
@@ -170,7 +177,7 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
     for (int r0 = 0; r0 < R; r0 += CH) {
         const int rend = R - r0 < CH ? R - r0 : CH;
         int own_j[CH], idx[CH];         // list | list position << 8; the candidate's grid index
-        uint64_t pt[CH];                // the candidate's grid point
+        decltype(ev.point(0)) pt[CH];   // the candidate's grid point
         // all CH slots walk and read, also past the last round (their candidates are real; only the rounds up to R
         // are evaluated), so neither pass branches on the round count
 #pragma unroll

@@ -28,7 +28,7 @@ struct Tabs {
     bool ok = false;
     uint64_t *grid = nullptr;   // search grid
     int32_t *map = nullptr;     // full key map (2-bit keys, 43692; 3-bit keys, 4096)
-    int32_t *map3 = nullptr;    // 8-value types: the map re-indexed by base-3 keys (6561)
+    int32_t *map3 = nullptr;    // the staged map, off-grid entries packed: base-3 keys (6561) or 3-bit keys (4096)
     uint16_t *neigh = nullptr;
     int grid_size = 0, map_size = 0, neigh_len = 0;
     uint64_t *dq = nullptr;     // dequantizer grid (record 1000 + type)
@@ -111,7 +111,7 @@ bool valid_search(int t, const std::vector<uint64_t> &grid, const std::vector<in
         if (off >= NL) return false;
         const int cnt = neigh[off];
         if (cnt < 1 || off + cnt >= NL) return false;
-        if (e8 && (off + 1 >= (1 << M3_OFF_BITS) || cnt >= (1 << (31 - M3_OFF_BITS)))) return false;
+        if (off + 1 >= (1 << M3_OFF_BITS) || cnt >= (1 << (31 - M3_OFF_BITS))) return false;
         for (int j = 1; j <= cnt; ++j)
             if (neigh[off + j] >= G) return false;
     }
@@ -380,13 +380,19 @@ extern "C" int gpuq_init(const char *tables, int device) {
             t.grid_size = (int)r.grid.size();
             t.map_size = (int)r.map.size();
             t.neigh_len = (int)r.neigh.size();
-            if (eight_values(r.type)) {
-                std::vector<int32_t> m3(6561);
-                for (int k = 0; k < 6561; ++k) {
-                    int u = 0, rr = k;
-                    for (int i = 0; i < 8; ++i) { u |= (rr % 3) << (2 * i); rr /= 3; }
+            {
+                // the map the kernels stage: for the 8-value types re-indexed by base-3 keys (6561), for the 4-value
+                // types the 4096 3-bit keys as they are; off-grid entries pack the list offset and its length
+                // (m3_off / m3_cnt), checked by valid_search
+                const bool e8 = eight_values(r.type);
+                std::vector<int32_t> m3(e8 ? 6561 : 4096);
+                for (int k = 0; k < (int)m3.size(); ++k) {
+                    int u = k, rr = k;
+                    if (e8) {
+                        u = 0;
+                        for (int i = 0; i < 8; ++i) { u |= (rr % 3) << (2 * i); rr /= 3; }
+                    }
                     const int m = r.map[u];
-                    // off-grid: the list offset and its length packed (m3_off / m3_cnt), checked by valid_search
                     m3[k] = m >= 0 ? m : -1 - ((-m - 1) | ((int)r.neigh[-(int64_t)m - 1] << M3_OFF_BITS));
                 }
                 if (!upload(&t.map3, m3)) return 4;

@@ -2,8 +2,10 @@
 //
 // Semantics: ggml's quantize_row_iq3_xxs_impl / quantize_row_iq3_s_impl as the reference restates them
 // (gpuq/gpuq.hip:971-1283). Per lane: one 32-weight sub-block of eight 4-value groups. The whole 4096-entry 3-bit
-// key map (every key is reachable: levels 0..7) and the grid (uint32 points, byte i = 2l+1) sit in LDS; neighbour
-// lists stay in HBM. A group's levels are kept as its point's 4 bytes, one dword a group.
+// key map (every key is reachable: levels 0..7; off-grid entries packed with their list's offset and length) and the
+// grid (uint32 points, byte i = 2l+1) sit in LDS; neighbour lists stay in HBM. A group's levels are kept as its
+// point's 4 bytes, one dword a group. The neighbour searches are wave-wide (coop.cuh): a trial's 8 groups in two
+// calls of 4 lists a lane, each list with its own staged values.
 #pragma once
 #include "iq2.cuh"
 
@@ -31,7 +33,7 @@ template <int GRID> struct Iq4Tab {
         uint32_t *gd = (uint32_t *)lds;
         for (int i = threadIdx.x; i < GRID; i += WG_THREADS) gd[i] = (uint32_t)p.grid[i];
         int32_t *md = (int32_t *)(lds + GRIDB);
-        for (int i = threadIdx.x; i < NKEY8; i += WG_THREADS) md[i] = p.map[i];
+        for (int i = threadIdx.x; i < NKEY8; i += WG_THREADS) md[i] = p.map3[i];
     }
     static DEV const uint32_t *grid(const uint8_t *lds) { return (const uint32_t *)lds; }
     static DEV const int32_t *map(const uint8_t *lds) { return (const int32_t *)(lds + GRIDB); }
@@ -44,25 +46,22 @@ DEV int key3_of_point(uint32_t pt) {
     return u;
 }
 
-// iq3_find_best_neighbour (gpuq/gpuq.hip:971-992)
-DEV int nb_best4(const uint16_t *nb, const uint32_t *grid, const float *xv, const float *wa, float scale) {
-    const int cnt = nb[0];
-    float best = FLT_MAX;
-    int gi = -1;
-    for (int j = 1; j <= cnt; ++j) {
-        const int idx = nb[j];
-        const uint32_t pt = grid[idx];
+// iq3_find_best_neighbour's distance of one grid point (gpuq/gpuq.hip:971-992) for an owner's staged values
+// (st[0..3] the x's, st[4..7] the weights), in the serial scan's operation order
+struct EvalIq4 {
+    const uint32_t *grid;
+    DEV uint32_t point(int idx) const { return grid[idx]; }
+    DEV float operator()(const float *st, float scale, uint32_t pt) const {
         float d2 = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float q = (float)((pt >> (8 * i)) & 0xffu);
-            const float diff = scale * q - xv[i];
-            d2 += wa[i] * diff * diff;
+            const float diff = scale * q - st[i];
+            d2 += st[4 + i] * diff * diff;
         }
-        if (d2 < best) { best = d2; gi = idx; }
+        return d2;
     }
-    return gi;
-}
+};
 
 DEV int group_key8(const float *xv, float id) {
     int u = 0;
@@ -71,10 +70,56 @@ DEV int group_key8(const float *xv, float id) {
     return u;
 }
 
-// the shared IQ3 32-weight search; returns the sub-block scale, P = its 8 group points, live = not skipped
+using Iq3WS = CoopWSM<4, 8, true>;
+constexpr int IQ3_CH = 4;       // rounds a chunk of the neighbour search
+
+// The 8 groups' points of every lane at one scale (all lanes call it together): a group with act[k] takes the grid
+// point of its key (id) if the key is on the grid, else the winner of its neighbour list (the distances at `scale`);
+// 4 groups a wave-wide call, each list with its group's staged values. A search that accepts nothing flags the error
+// (the reference traps) and yields point 0. P[k] and og[k] (the key was on the grid) are written where act[k].
+template <int GRID>
+DEV void iq3_points(const bool (&act)[8], float id, float scale, const float (&xval)[32], const float (&waux)[32],
+                    const int32_t *map, const uint32_t *grid, const QParams &p, Iq3WS &ws, uint32_t (&P)[8],
+                    bool (&og)[8]) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        int mk[4], cnt[4], off[4], gi[4];
+        float sc[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int k = 4 * h + m;
+            mk[m] = 0;
+            if (act[k]) mk[m] = map[group_key8(xval + 4 * k, id)];
+            const bool srch = act[k] && mk[m] < 0;
+            cnt[m] = srch ? m3_cnt(mk[m]) : 0;
+            off[m] = srch ? m3_off(mk[m]) : 0;
+            sc[m] = scale;
+            if (srch) coop_stage<4>(ws, xval + 4 * k, waux + 4 * k, lane_id() * 4 + m);
+        }
+        coop_search_m<4, IQ3_CH>(cnt, off, sc, p.neigh, p.neigh_len, ws, EvalIq4{grid}, gi);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int k = 4 * h + m;
+            if (!act[k]) continue;
+            og[k] = mk[m] >= 0;
+            int g = mk[m];
+            if (g < 0) {
+                g = gi[m];
+                if (g < 0) {
+                    flag_err(p);
+                    g = 0;
+                }
+            }
+            P[k] = grid[g];
+        }
+    }
+}
+
+// the shared IQ3 32-weight search (every lane of the wave runs it: the neighbour searches are wave-wide); returns
+// the sub-block scale, P = its 8 group points, live = not skipped
 template <bool XXS, int GRID>
 DEV float iq3_search(const float (&x)[32], const float (&qv)[32], float sigma2, const QParams &p, const uint8_t *lds,
-                     uint32_t (&P)[8], uint32_t (&bsg)[4], bool &live) {
+                     Iq3WS &ws, uint32_t (&P)[8], uint32_t (&bsg)[4], bool &live) {
     const uint32_t *grid = Iq4Tab<GRID>::grid(lds);
     const int32_t *map = Iq4Tab<GRID>::map(lds);
     float weight[32], waux[32], xval[32];
@@ -91,29 +136,27 @@ DEV float iq3_search(const float (&x)[32], const float (&qv)[32], float sigma2, 
 #pragma unroll
     for (int k = 0; k < 8; ++k) P[k] = 0x01010101u;          // L = 0
     live = XXS ? !(mx < EPS_IQ3XXS) : (mx != 0.f);
-    if (!live) return 0.f;
     float best = 0;
-    float scale = mx / 15;
-    bool on_grid[8];
+    float scale = live ? mx / 15 : 0.f;
+    bool on_grid[8], act[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) on_grid[k] = XXS;             // (IQ3_S starts from "not on the grid")
+    for (int k = 0; k < 8; ++k) {
+        on_grid[k] = XXS;                                     // (IQ3_S starts from "not on the grid")
+        act[k] = live;
+    }
     constexpr int NT = XXS ? 15 : 9;
+#pragma unroll 1
     for (int is = -NT; is <= NT; ++is) {
         const float id = (15 + is * 0.2f) / mx;
         const float this_scale = 1 / id;
         uint32_t Pa[8];
         bool og[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int m = map[group_key8(xval + 4 * k, id)];
-            og[k] = m >= 0;
-            const int gi = m >= 0 ? m : nb_best4(p.neigh + (-m - 1), grid, xval + 4 * k, waux + 4 * k, this_scale);
-            if (gi < 0) flag_err(p);
-            Pa[k] = grid[gi < 0 ? 0 : gi];
-        }
+        for (int k = 0; k < 8; ++k) { Pa[k] = 0x01010101u; og[k] = false; }
+        iq3_points<GRID>(act, id, this_scale, xval, waux, map, grid, p, ws, Pa, og);
         float sumqx, sumq2;
         sums_q<32>(weight, xval, Pa, sumqx, sumq2);
-        if (sumq2 > 0 && sumqx * sumqx > best * sumq2) {
+        if (live && sumq2 > 0 && sumqx * sumqx > best * sumq2) {
             scale = sumqx / sumq2;
             best = scale * sumqx;
 #pragma unroll
@@ -123,19 +166,18 @@ DEV float iq3_search(const float (&x)[32], const float (&qv)[32], float sigma2, 
     bool any_off = false;
 #pragma unroll
     for (int k = 0; k < 8; ++k) any_off |= !on_grid[k];
-    if (any_off && scale > 0) {
+    const bool fin = live && any_off && scale > 0;
+    {
         const float id = 1 / scale;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            if (XXS && on_grid[k]) continue;                  // (IQ3_S re-searches every group)
-            const int m = map[group_key8(xval + 4 * k, id)];
-            const int gi = m >= 0 ? m : nb_best4(p.neigh + (-m - 1), grid, xval + 4 * k, waux + 4 * k, scale);
-            if (gi < 0) flag_err(p);
-            P[k] = grid[gi < 0 ? 0 : gi];
+        for (int k = 0; k < 8; ++k) act[k] = fin && !(XXS && on_grid[k]);   // (IQ3_S re-searches every group)
+        bool og[8];
+        iq3_points<GRID>(act, id, scale, xval, waux, map, grid, p, ws, P, og);
+        if (fin) {
+            float sumqx, sumq2;
+            sums_q<32>(weight, xval, P, sumqx, sumq2);
+            if (sumq2 > 0) scale = sumqx / sumq2;
         }
-        float sumqx, sumq2;
-        sums_q<32>(weight, xval, P, sumqx, sumq2);
-        if (sumq2 > 0) scale = sumqx / sumq2;
     }
     if (scale < 0) {
         scale = -scale;
@@ -147,7 +189,7 @@ DEV float iq3_search(const float (&x)[32], const float (&qv)[32], float sigma2, 
 
 // IQ3_XXS: block d qs[96] = 64 grid bytes, then 8 u32 signs-and-scales (98 bytes)
 struct KIQ3XXS : Iq4Tab<256> {
-    static constexpr int BS = QK, G = 8, N = 32, BB = 98;
+    static constexpr int BS = QK, G = 8, N = 32, BB = 98, WS = coop_wsm_bytes<4, 8, true>();
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
                           const QParams &p) {
         const int32_t *map = Iq4Tab<256>::map(lds);
@@ -158,7 +200,7 @@ struct KIQ3XXS : Iq4Tab<256> {
         const float sigma2 = 2 * grp_chain_sum<G, N>(sq, g) / QK;
         uint32_t P[8], bsg[4];
         bool live;
-        const float scale = iq3_search<true, 256>(x, qv, sigma2, p, lds, P, bsg, live);
+        const float scale = iq3_search<true, 256>(x, qv, sigma2, p, lds, *(Iq3WS *)wave_ws<KIQ3XXS>(img), P, bsg, live);
         const float max_scale = grp_max<G>(live ? scale : 0.f);
         if (!max_scale) return;                               // qs all zero, d = 0
         uint32_t q3lo = 0, q3hi = 0, sas = 0;
@@ -186,7 +228,7 @@ struct KIQ3XXS : Iq4Tab<256> {
 // IQ3_S: block d qs[64] qh[8] signs[32] scales[4] (110 bytes). A skipped (all-zero) sub-block does not advance the
 // qs / signs cursors (ggml's quirk, kept by the reference): the next live sub-block takes its slot.
 struct KIQ3S : Iq4Tab<512> {
-    static constexpr int BS = QK, G = 8, N = 32, BB = 110;
+    static constexpr int BS = QK, G = 8, N = 32, BB = 110, WS = coop_wsm_bytes<4, 8, true>();
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
                           const QParams &p) {
         const int32_t *map = Iq4Tab<512>::map(lds);
@@ -197,7 +239,7 @@ struct KIQ3S : Iq4Tab<512> {
         const float sigma2 = 2 * grp_chain_sum<G, N>(sq, g) / QK;
         uint32_t P[8], bsg[4];
         bool live;
-        const float scale = iq3_search<false, 512>(x, qv, sigma2, p, lds, P, bsg, live);
+        const float scale = iq3_search<false, 512>(x, qv, sigma2, p, lds, *(Iq3WS *)wave_ws<KIQ3S>(img), P, bsg, live);
         // the slot of this sub-block: the number of live sub-blocks before it
         const uint64_t bal = __ballot(live);
         const int gbase = lane_id() & ~(G - 1);
