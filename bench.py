@@ -7,7 +7,8 @@ One "step" is one pass of the quantizer over one workload tensor already residen
 gpuq_requantize_dev: source bytes decoded in registers, quantized, blocks written to HBM). The headline line is the
 Q4_K-with-imatrix workload on a 2048 x 7168 BF16 tensor (N(0, 0.02) plus 0.1% outliers at +-8 sigma, a log-normal
 imatrix); `per_type` adds Q6_K on the same tensor, Q8_0 on a 4096 x 4096 F32 tensor, IQ2_XXS on 256 x 2048 x 7168
-BF16 experts and IQ1_S / IQ1_M on 384 x 2048 x 7168 MXFP4 experts. Kernel time comes from HIP events on the launch
+BF16 experts and IQ1_S / IQ1_M on 384 x 2048 x 7168 MXFP4 experts; `other_types` the remaining nine types on the
+headline tensor (GPU rate, roofline, byte spot check on 64 rows). Kernel time comes from HIP events on the launch
 stream; inputs that fit the 256 MB Infinity Cache are rotated over enough copies that every launch reads HBM.
 
 Each entry carries a roofline (HBM bytes for Q8_0, VALU operations for the searches: the sequential algorithm's
@@ -350,6 +351,19 @@ def main():
             per[name] = e
             del out_t
         del c1
+        # every other type on the same BF16 tensor: GPU rate, roofline (oracle-counted ops) and a byte spot check on
+        # 64 rows (no CPU timing)
+        other = {}
+        for name in ("Q2_K", "Q3_K", "Q5_K", "IQ4_NL", "IQ4_XS", "IQ2_XS", "IQ2_S", "IQ3_XXS", "IQ3_S"):
+            typ = getattr(gpuq, name)
+            log("other type: %s on %s" % (name, c2.name))
+            ms_t, out_t = time_gpu(torch, gq, gpuq, c2, typ, ksteps, 1)
+            e = {"value": round(c2.n / (ms_t / 1e3) / 1e6, 1), "unit": "Mweights/s", "ms_per_step": round(ms_t, 4),
+                 "steps": ksteps}
+            e.update(cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, c2, typ, ms_t, out_t, 64, False))
+            other[name] = e
+            del out_t
+        line["other_types"] = {"workload": c2.name, "types": other}
         nthr = cpu_threads()
         nexp_c3 = args.experts or 256
         c3 = wl_c3(torch, gpuq, nexp_c3)

@@ -313,9 +313,43 @@ struct KIQ2XXS : Iq8Tab<256> {
 // IQ2_S's one-shell neighbour lists are short (a few rounds a call): chunks of 2 rounds waste the least
 // (IQ2_XS's two-shell lists are longer: 8 rounds a chunk, measured 3% faster than 2)
 template <int GRID> constexpr int ch16() { return GRID == 512 ? 8 : 2; }
+// the search workspace of the 16-weight types: the lane's two groups as two lists, each with its staged values
+using Iq16WS = CoopWSM<2, 16, true>;
+
+// the two groups' grid indices of every lane at one scale (all lanes call it together): a group with act[k] takes
+// the grid point of its key (id) if the key is on the grid, else the winner of its neighbour list (the distances at
+// `scale`), one wave-wide call for both groups (their values staged beforehand, list lane*2 + k). A search that
+// accepts nothing flags the error (the reference traps) and yields index 0. Inactive groups get 0.
+template <int GRID>
+DEV void iq2_16_points(const bool (&act)[2], float id, float scale, const float (&xval)[16], const int32_t *map3,
+                       const QParams &p, const uint64_t *grid, Iq16WS &ws, int (&gi)[2], bool (&og)[2]) {
+    int mk[2], cnt[2], off[2], g[2];
+    float sc[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        mk[k] = act[k] ? map3[group_key3(xval + 8 * k, id)] : 0;
+        og[k] = mk[k] >= 0;
+        cnt[k] = act[k] && mk[k] < 0 ? m3_cnt(mk[k]) : 0;
+        off[k] = act[k] && mk[k] < 0 ? m3_off(mk[k]) : 0;
+        sc[k] = scale;
+    }
+    coop_search_m<2, ch16<GRID>()>(cnt, off, sc, p.neigh, p.neigh_len, ws, EvalIq8{grid}, g);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        gi[k] = mk[k];
+        if (act[k] && mk[k] < 0) {
+            gi[k] = g[k];
+            if (g[k] < 0) {
+                flag_err(p);
+                gi[k] = 0;
+            }
+        }
+    }
+}
+
 template <bool PARITY, int GRID>
 DEV float iq2_16_search(const float (&x)[16], const float (&qv)[16], float sigma2, float eps, const QParams &p,
-                        const uint8_t *lds, CoopWS &ws, int (&gidx)[2], uint32_t (&bsg)[2], bool &live) {
+                        const uint8_t *lds, Iq16WS &ws, int (&gidx)[2], uint32_t (&bsg)[2], bool &live) {
     const uint64_t *grid = Iq8Tab<GRID>::grid(lds);
     const int32_t *map3 = Iq8Tab<GRID>::map3(lds);
     float weight[16], waux[16], xval[16];
@@ -336,19 +370,20 @@ DEV float iq2_16_search(const float (&x)[16], const float (&qv)[16], float sigma
     float scale = mx / 5;
     int P[2] = {-1, -1};        // accepted trial's groups as grid indices; -1: all levels 0 (no trial accepted yet)
     bool on_grid[2] = {true, true};
+    // the two groups' values, staged once for all the trials and the final pass
+#pragma unroll
+    for (int k = 0; k < 2; ++k) coop_stage<8>(ws, xval + 8 * k, waux + 8 * k, lane_id() * 2 + k);
+    const bool act_live[2] = {live, live};
 #pragma unroll 1
     for (int is = -9; is <= 9; ++is) {
         const float id = (5 + is * 0.1f) / mx;
         const float this_scale = 1 / id;
         int Pa[2];
         bool og[2];
+        iq2_16_points<GRID>(act_live, id, this_scale, xval, map3, p, grid, ws, Pa, og);
         float sumqx = 0, sumq2 = 0;
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            Pa[k] = group_point_w<ch16<GRID>()>(live, group_key3(xval + 8 * k, id), map3, p, grid, xval + 8 * k, waux + 8 * k,
-                                  this_scale, ws, og[k]);
-            sums_q8(weight + 8 * k, xval + 8 * k, grid[Pa[k]], sumqx, sumq2);
-        }
+        for (int k = 0; k < 2; ++k) sums_q8(weight + 8 * k, xval + 8 * k, grid[Pa[k]], sumqx, sumq2);
         if (live && sumq2 > 0 && sumqx * sumqx > best * sumq2) {
             scale = sumqx / sumq2;
             best = scale * sumqx;
@@ -362,14 +397,14 @@ DEV float iq2_16_search(const float (&x)[16], const float (&qv)[16], float sigma
     const bool fin = live && (!on_grid[0] || !on_grid[1]) && scale > 0;
     {
         const float id = 1 / scale;
+        const bool act[2] = {fin && !on_grid[0], fin && !on_grid[1]};
+        int gi[2];
+        bool og[2];
+        iq2_16_points<GRID>(act, id, scale, xval, map3, p, grid, ws, gi, og);
         float sumqx = 0, sumq2 = 0;
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
-            const bool act = fin && !on_grid[k];
-            bool og;
-            const int gi = group_point_w<ch16<GRID>()>(act, group_key3(xval + 8 * k, id), map3, p, grid, xval + 8 * k,
-                                         waux + 8 * k, scale, ws, og);
-            if (act) P[k] = gi;
+            if (act[k]) P[k] = gi[k];
             sums_q8(weight + 8 * k, xval + 8 * k, grid[P[k] < 0 ? 0 : P[k]], sumqx, sumq2);
         }
         if (fin && sumq2 > 0) scale = sumqx / sumq2;
@@ -393,7 +428,7 @@ DEV float iq2_16_search(const float (&x)[16], const float (&qv)[16], float sigma
 
 // IQ2_S: block d qs[64] (32 grid bytes, 32 sign bytes) qh[8] scales[8] (82 bytes); lane g = 16-weight sub-block g
 struct KIQ2S : Iq8Tab<1024> {
-    static constexpr int BS = QK, G = 16, N = 16, BB = 82, WS = COOP_WS_BYTES;
+    static constexpr int BS = QK, G = 16, N = 16, BB = 82, WS = coop_wsm_bytes<2, 16, true>();
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
                           const QParams &p) {
         float qv[N], sq[N];
@@ -405,7 +440,7 @@ struct KIQ2S : Iq8Tab<1024> {
         uint32_t bsg[2];
         bool live;
         const float scale = iq2_16_search<false, 1024>(x, qv, sigma2, EPS_IQ2S, p, lds,
-                                                       *(CoopWS *)wave_ws<KIQ2S>(img), gidx, bsg, live);
+                                                       *(Iq16WS *)wave_ws<KIQ2S>(img), gidx, bsg, live);
         if (live) {
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
@@ -427,7 +462,7 @@ struct KIQ2S : Iq8Tab<1024> {
 
 // IQ2_XS: block d qs[32] u16 scales[8] (74 bytes); qs[2g+k] = grid index | signs << 9
 struct KIQ2XS : Iq8Tab<512> {
-    static constexpr int BS = QK, G = 16, N = 16, BB = 74, WS = COOP_WS_BYTES;
+    static constexpr int BS = QK, G = 16, N = 16, BB = 74, WS = coop_wsm_bytes<2, 16, true>();
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
                           const QParams &p) {
         float qv[N], sq[N];
@@ -439,7 +474,7 @@ struct KIQ2XS : Iq8Tab<512> {
         uint32_t bsg[2];
         bool live;
         const float scale = iq2_16_search<true, 512>(x, qv, sigma2, EPS_GROUP, p, lds,
-                                                     *(CoopWS *)wave_ws<KIQ2XS>(img), gidx, bsg, live);
+                                                     *(Iq16WS *)wave_ws<KIQ2XS>(img), gidx, bsg, live);
         const float max_scale = grp_max<G>(live ? scale : 0.f);
         if (!max_scale) return;                     // qs all zero, scales zero, d = 0
         if (live) {
