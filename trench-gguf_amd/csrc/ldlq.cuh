@@ -155,13 +155,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     const double *abase = Es + m * ne1 + row0 + le;          // + k * R + 16 j
     const double *bbase = Um + col0 + le;                     // + (c0 + k) * ne0 + 16 j
     double av[8], bv[8];
+    // a tile inside the matrix (the usual case) loads unguarded: no per-element branches
+    const bool full = row0 + LDLQ_TM <= ne1 && col0 + LDLQ_TN <= ce;
     auto load = [&](int k0) {
         const double *ap = abase + (int64_t)(k0 + lk) * R;
         const double *bp = bbase + (c0 + k0 + lk) * ne0;
+        if (full) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) av[j] = row0 + le + 16 * j < ne1 ? ap[16 * j] : 0.0;
+            for (int j = 0; j < 8; ++j) av[j] = ap[16 * j];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) bv[j] = col0 + le + 16 * j < ce ? bp[16 * j] : 0.0;
+            for (int j = 0; j < 8; ++j) bv[j] = bp[16 * j];
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) av[j] = row0 + le + 16 * j < ne1 ? ap[16 * j] : 0.0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) bv[j] = col0 + le + 16 * j < ce ? bp[16 * j] : 0.0;
+        }
     };
     auto stash = [&](int buf) {
 #pragma unroll
@@ -195,9 +204,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         buf ^= 1;
     }
     // epilogue: every W value of the wave's sub-tile is read before the first store (a store between the reads
-    // would make each read wait for the one before it); a tile inside the matrix (the usual case) runs unguarded, so
-    // the stores need no per-element branches (and their waits no conservative counts)
-    const bool full = row0 + LDLQ_TM <= ne1 && col0 + LDLQ_TN <= ce;
+    // would make each read wait for the one before it); a full tile runs unguarded, so the stores need no
+    // per-element branches (and their waits no conservative counts)
     float wv[4][4][4];
     if (full) {
 #pragma unroll
