@@ -679,20 +679,22 @@ struct KQ80 {
 __constant__ float k_iq4f[16] = {-127.f, -104.f, -83.f, -65.f, -49.f, -35.f, -22.f, -10.f,
                                  1.f,    13.f,   25.f,  38.f,  53.f,  69.f,  89.f,  113.f};
 
-// best_index_int8 over the IQ4 codebook: the binary search of the reference with its data-dependent trip count
-// run as 4 predicated steps; codebook values come from a 16-float LDS copy
-DEV int iq4_index(float x, const float *kv) {
-    if (x <= kv[0]) return 0;
-    if (x >= kv[15]) return 15;
-    int ml = 0, mu = 15;
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        if (mu - ml > 1) {
-            const int mav = (ml + mu) / 2;
-            if (x < kv[mav]) mu = mav; else ml = mav;
-        }
-    }
-    return x - kv[mu - 1] < kv[mu] - x ? mu - 1 : mu;
+// best_index_int8 over the IQ4 codebook (gpuq/gpuq.hip:1286-1295). For strictly increasing values the reference's
+// binary search always ends at the interval kv[ml] <= x < kv[ml+1] (ml = 15 for x >= kv[15] and for NaN, which its
+// false x < kv[mav] tests move up; ml = 0 for x < kv[1]), so four branch-free halving steps find the same ml; then
+// the nearer end with the reference's tie rule. (Checked equal to the reference's search on all 2^32 floats.)
+// Codebook values come from a 16-float LDS copy.
+DEV int iq4_index(float x, const float *kv, float &q) {
+    int ml = 0;
+    ml += !(x < kv[8]) ? 8 : 0;
+    ml += !(x < kv[ml + 4]) ? 4 : 0;
+    ml += !(x < kv[ml + 2]) ? 2 : 0;
+    ml += !(x < kv[ml + 1]) ? 1 : 0;
+    const int mu = ml < 15 ? ml + 1 : 15;
+    const float lo = kv[ml], hi = kv[mu];
+    const bool down = ml == 15 || x - lo < hi - x;
+    q = down ? lo : hi;
+    return down ? ml : mu;
 }
 
 // one 32-weight sub-block's scale search; fills Lb, returns the scale (0 for a negligible block)
@@ -710,9 +712,9 @@ DEV float iq4_block(const float (&xb)[32], const float (&weight)[32], Lv<32> &Lb
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
         const float al = id * xb[j];
-        const int l = iq4_index(al, kv);
+        float q;
+        const int l = iq4_index(al, kv, q);
         Lb.put(j, (uint32_t)l);
-        const float q = kv[l];
         const float w = weight[j];
         sumqx += w * q * xb[j];
         sumq2 += w * q * q;
@@ -725,8 +727,8 @@ DEV float iq4_block(const float (&xb)[32], const float (&weight)[32], Lv<32> &Lb
 #pragma unroll
         for (int j = 0; j < 32; ++j) {
             const float al = id * xb[j];
-            const int l = iq4_index(al, kv);
-            const float q = kv[l];
+            float q;
+            (void)iq4_index(al, kv, q);
             const float w = weight[j];
             sumqx += w * q * xb[j];
             sumq2 += w * q * q;
@@ -776,7 +778,7 @@ struct KIQ4XS {
         const float dl = d * l;
         const float idl = dl ? 1 / dl : 0.f;
 #pragma unroll
-        for (int j = 0; j < 32; ++j) Lb.put(j, (uint32_t)iq4_index(idl * x[j], kv));
+        for (int j = 0; j < 32; ++j) { float q; Lb.put(j, (uint32_t)iq4_index(idl * x[j], kv, q)); }
         l += 32;
         if (g == 0) img_or16(img, boff, d16);
         img_or16(img, boff + 2, (uint32_t)((l >> 4) << (2 * g)));
@@ -817,7 +819,7 @@ struct KIQ4NL {
         img_or16(img, boff, f2h(s));
         const float id = s ? 1 / s : 0;
 #pragma unroll
-        for (int j = 0; j < 32; ++j) Lb.put(j, (uint32_t)iq4_index(id * x[j], kv));
+        for (int j = 0; j < 32; ++j) { float q; Lb.put(j, (uint32_t)iq4_index(id * x[j], kv, q)); }
         uint32_t wv[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) wv[k] = Lb.w[k] | (Lb.w[k + 4] << 4);
