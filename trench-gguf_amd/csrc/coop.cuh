@@ -64,11 +64,11 @@ template <class W> DEV void coop_fetch(const W &ws, int owner, float (&st)[16]) 
 }
 
 // a / b for 0 <= a < 2^20, 1 <= b < 2^12: a float quotient (hardware reciprocal, within 1 of the floor), corrected
-// to the floor
+// to the floor; the products stay below 2^32 with 24-bit operands (full-rate multiplies)
 DEV int div_small(int a, int b) {
     int q = (int)((float)a * __builtin_amdgcn_rcpf((float)b));
-    q += (q + 1) * b <= a;
-    q -= q * b > a;
+    q += (int)__umul24((unsigned)(q + 1), (unsigned)b) <= a;
+    q -= (int)__umul24((unsigned)q, (unsigned)b) > a;
     return q;
 }
 
@@ -145,11 +145,11 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
         int start = incl - tot;                         // the list's first position
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-            if (cnt[m] > 0) {                           // walkers L with start <= L*R < start + cnt begin in list m
-                const int lf = div_small(start + R - 1, R);
-                const int ll = div_small(start + cnt[m] - 1, R);
-                for (int L = lf; L <= ll && L < 64; ++L) ws.mark[L] = (lane * M + m) | ((L * R - start) << 8);
-            }
+            // walkers L with start <= L*R < start + cnt begin in list m (none when cnt == 0: lf > ll)
+            const int lf = div_small(start + R - 1, R);
+            const int ll = div_small(start + cnt[m] - 1, R);
+            for (int L = lf; L <= ll && L < 64; ++L)
+                ws.mark[L] = (lane * M + m) | (((int)__umul24((unsigned)L, (unsigned)R) - start) << 8);
             start += cnt[m];
         }
     }
