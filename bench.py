@@ -23,6 +23,8 @@ import os
 import sys
 import time
 
+import numpy as np
+
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "trench-gguf_amd"))
 sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -203,6 +205,23 @@ def bench_ldlq(torch, gq, gpuq, orc, steps, want_cpu, nexp):
     return e
 
 
+_sleep_per_ms = []
+
+
+def hold_gpu(torch, ms):
+    """keep the current stream busy for about `ms` (torch's spin kernel, calibrated once), so that launches timed
+    after it run back to back instead of waiting for the host to issue each (a Q8_0 launch takes ~20 us)"""
+    if not _sleep_per_ms:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(1000)
+        e0.record()
+        torch.cuda._sleep(1 << 20)
+        e1.record()
+        torch.cuda.synchronize()
+        _sleep_per_ms.append((1 << 20) / max(e0.elapsed_time(e1), 1e-3))
+    torch.cuda._sleep(int(ms * _sleep_per_ms[0]))
+
+
 def time_gpu(torch, gq, gpuq, wl, typ, steps, warmup):
     """average kernel time (ms) of gpuq_requantize_dev over `steps` launches, HIP events on the launch stream"""
     bpw = {gpuq.F32: 4.0, gpuq.BF16: 2.0, gpuq.MXFP4: 17 / 32}[wl.src]
@@ -226,10 +245,13 @@ def time_gpu(torch, gq, gpuq, wl, typ, steps, warmup):
         launch(i)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    hold_gpu(torch, 2.0 + 0.05 * steps)     # the host enqueues every timed launch before the GPU reaches e0
     e0.record(stream)
     for i in range(steps):
         launch(warmup + i)
     e1.record(stream)
+    if e0.query():
+        log("note: the GPU reached the timed launches before the host had enqueued them all")
     torch.cuda.synchronize()
     if gq.gpuq_take_error():
         raise RuntimeError("a search reported no candidate (%s)" % gpuq.TYPE_NAMES[typ])
@@ -237,6 +259,37 @@ def time_gpu(torch, gq, gpuq, wl, typ, steps, warmup):
     result = outs[(warmup + steps - 1) % len(outs)]
     del raws[1:]
     return ms, result
+
+
+def host_api(torch, gq, gpuq, wl, typ, nmat, dev_out, reps=3):
+    """PCIe-inclusive rate of the host entry point gpuq_requantize_batch on the first `nmat` matrices of the workload:
+    source bytes in pageable host memory, blocks back into host memory (copies overlapped with the kernels); its bytes
+    must equal the device entry point's"""
+    u8 = wl.raw.view(torch.uint8).reshape(-1)
+    per_src = u8.numel() // wl.nmat
+    raw = u8[:nmat * per_src].cpu().numpy()
+    im = None if wl.imatrix is None else np.ascontiguousarray(wl.imatrix[:nmat].cpu().numpy())
+    per_out = wl.nrow * wl.ncol // gpuq.BLOCK[typ] * gq.gpuq_block_bytes(typ)
+    out = np.empty(nmat * per_out, dtype=np.uint8)
+
+    def call():
+        got = gq.gpuq_requantize_batch(wl.src, raw.ctypes.data, typ, out.ctypes.data, nmat, wl.nrow, wl.ncol,
+                                       None if im is None else im.ctypes.data)
+        if got != out.nbytes:
+            raise RuntimeError("gpuq_requantize_batch failed for %s" % gpuq.TYPE_NAMES[typ])
+    call()                                                        # (grows the staging buffers)
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        call()
+        ts.append(time.perf_counter() - t0)
+    ms = 1e3 * sorted(ts)[len(ts) // 2]
+    same = bool(np.array_equal(out, dev_out.reshape(-1)[:out.nbytes].cpu().numpy()))
+    nw = nmat * wl.nrow * wl.ncol
+    return {"entry_point": "gpuq_requantize_batch", "matrices": nmat, "value": round(nw / (ms / 1e3) / 1e6, 1),
+            "unit": "Mweights/s", "ms_per_call": round(ms, 3), "calls": reps,
+            "host_bytes_in": int(raw.nbytes), "host_bytes_out": int(out.nbytes),
+            "identical_to_device_entry_point": same}
 
 
 def host_sample(torch, wl, rows):
@@ -343,6 +396,9 @@ def main():
     if "cpu_baseline" in head:
         line["cpu_baseline"] = head["cpu_baseline"]
     line["sample_identical_to_oracle"] = head["sample_identical_to_oracle"]
+    log("host entry point: Q4_K on %s" % c2.name)
+    line["host_api"] = {"note": "PCIe-inclusive, pageable host memory in and out; not the value",
+                        "Q4_K": host_api(torch, gq, gpuq, c2, gpuq.Q4_K, 1, out)}
     per = {}
     if not args.quick:
         ksteps = max(1, min(args.steps, 5))
@@ -386,6 +442,8 @@ def main():
             if "cpu_baseline" in e:
                 e["speedup_vs_cpu"] = round(e["value"] / e["cpu_baseline"]["value"], 1)
             per[name] = e
+            log("host entry point: %s on 16 experts" % name)
+            line["host_api"][name] = host_api(torch, gq, gpuq, c3, typ, min(16, c3.nmat), out_t)
             del out_t
         del c3
         torch.cuda.empty_cache()

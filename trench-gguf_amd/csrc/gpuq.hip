@@ -8,7 +8,10 @@
 
 #include <cstdio>
 #include <cstring>
+#include <algorithm>
+#include <cstdlib>
 #include <mutex>
+#include <thread>
 #include <vector>
 
 #include "common.cuh"
@@ -54,7 +57,7 @@ struct Buf {
         return true;
     }
 };
-Buf g_raw, g_qw, g_out, g_f32, g_es;
+Buf g_qw, g_es;
 
 bool is_search_type(int t) {
     return t == T_IQ2_XXS || t == T_IQ2_XS || t == T_IQ2_S || t == T_IQ1_S || t == T_IQ3_XXS || t == T_IQ3_S;
@@ -250,40 +253,174 @@ bool type_ok(int type, int64_t n_per_row, bool with_imatrix) {
     return n_per_row > 0 && n_per_row % block_len(type) == 0;
 }
 
-// the host API's body: raw bytes of nmat x nrow x n_per_row values (src encoding) -> dst (host), synchronous
+// ------------------------------------------------------------------ the host API's streamed pipeline
+// The reference's host entry points copy the whole input to the device, quantize, and copy the whole output back,
+// one synchronous step after another (gpuq/gpuq.hip:2160-2250). Here one call is cut into chunks of whole rows
+// (whole matrices when a matrix fits the chunk, else rows of one matrix, so every chunk keeps its imatrix row), and
+// the chunks run through three slots: while chunk i is quantized, chunk i+1's source bytes go into pinned memory
+// and on to the device, and chunk i-1's blocks come back; the host takes a chunk's blocks out of pinned memory two
+// chunks later, so that waiting for them never holds up the next chunk's copy in (PCIe, ~57 GB/s each way, is the
+// bound for the fast types). The bytes written equal those of one launch over the whole input: a block's result
+// depends only on its own values and its matrix's imatrix row.
+
+// pinned host memory (hipHostMalloc), kept for the process like the device buffers
+struct PinBuf {
+    void *p = nullptr;
+    size_t cap = 0;
+    bool grow(size_t need) {
+        if (need <= cap) return true;
+        if (p) (void)hipHostFree(p);
+        p = nullptr;
+        cap = 0;
+        if (hipHostMalloc(&p, need, hipHostMallocDefault) != hipSuccess) {
+            p = nullptr;
+            return false;
+        }
+        cap = need;
+        return true;
+    }
+};
+
+constexpr int NSLOT = 3;
+struct Slot {
+    Buf in, f32, out;                 // device: source bytes, decoded floats (F16 / Q8_0 sources), blocks
+    PinBuf pin_in, pin_out;
+    hipEvent_t copied = nullptr;      // the slot's H2D copy is done: pin_in may be refilled
+    hipEvent_t quantized = nullptr;   // the slot's kernels are done: in and f32 may be refilled, out is complete
+    hipEvent_t returned = nullptr;    // the slot's D2H copy is done: out may be rewritten, pin_out is complete
+    int64_t r0 = 0, rows = 0;         // the chunk the slot holds
+    bool used = false;
+};
+Slot g_slot[NSLOT];
+hipStream_t g_st_in = nullptr, g_st_q = nullptr, g_st_out = nullptr;   // default priority, non-blocking
+
+bool pipe_ready() {
+    if (g_st_out) return true;
+    for (hipStream_t *s : {&g_st_in, &g_st_q, &g_st_out})
+        if (hipStreamCreateWithFlags(s, hipStreamNonBlocking) != hipSuccess) return false;
+    for (Slot &s : g_slot)
+        for (hipEvent_t *e : {&s.copied, &s.quantized, &s.returned})   // (waits on them sleep rather than spin)
+            if (hipEventCreateWithFlags(e, hipEventDisableTiming | hipEventBlockingSync) != hipSuccess) return false;
+    return true;
+}
+
+// source bytes a chunk holds at most: GPUQ_STAGE_MB MiB (default 64; a chunk always holds at least one row)
+int64_t stage_bytes() {
+    const char *e = getenv("GPUQ_STAGE_MB");
+    long mb = e ? strtol(e, nullptr, 10) : 64;
+    if (mb < 1) mb = 64;
+    return (int64_t)mb << 20;
+}
+
+// memcpy over up to 16 threads, at least 1 MiB each (pageable <-> pinned staging: one thread moves ~27 GB/s, 16
+// about 110 GB/s, while PCIe takes ~57 GB/s each way)
+void par_copy(void *dst, const void *src, size_t n) {
+    constexpr size_t part_min = (size_t)1 << 20;
+    unsigned nt = std::thread::hardware_concurrency();
+    nt = nt == 0 ? 1 : (nt > 16 ? 16 : nt);
+    if ((size_t)nt > n / part_min) nt = (unsigned)(n / part_min);
+    if (nt <= 1) {
+        memcpy(dst, src, n);
+        return;
+    }
+    const size_t step = (n / nt + 4095) & ~(size_t)4095;
+    std::vector<std::thread> th;
+    size_t started = step;   // [0, step) is this thread's part; [step, started) went to other threads
+    try {
+        for (; started < n; started += step) {
+            const size_t b = started, len = n - b < step ? n - b : step;
+            th.emplace_back([=] { memcpy((char *)dst + b, (const char *)src + b, len); });
+        }
+    } catch (...) {   // a thread could not be started: copy what is left here
+        memcpy((char *)dst + started, (const char *)src + started, n - started);
+    }
+    memcpy(dst, src, step);
+    for (std::thread &t : th) t.join();
+}
+
+// the host API's body: raw bytes of nmat x nrow x n_per_row values (src encoding) -> dst (host); returns once dst
+// holds every block, or 0 on an error
 size_t quantize_host(int src, const void *raw, int type, void *dst, int64_t nmat, int64_t nrow, int64_t n_per_row,
                      const float *imatrix) {
     if (nmat <= 0 || nrow <= 0 || !type_ok(type, n_per_row, imatrix != nullptr)) return 0;
-    const int64_t n = nmat * nrow * n_per_row;
-    const int64_t rb = src_bytes(src, n);
-    if (!rb || n % 32) return 0;
+    const int64_t row_src = src_bytes(src, n_per_row);
+    if (!row_src || n_per_row % 32) return 0;
     std::lock_guard<std::mutex> lock(g_mu);
-    const int bs = block_len(type);
-    const int64_t nb_row = n_per_row / bs, nb_mat = nrow * nb_row, nunits = nmat * nb_mat;
-    const size_t out_bytes = (size_t)nunits * gpuq_block_bytes(type);
-    if (!g_raw.grow((size_t)rb + 16) || !g_out.grow(out_bytes + 16)) return 0;
-    if (hipMemcpy(g_raw.p, raw, (size_t)rb, hipMemcpyHostToDevice) != hipSuccess) return 0;
+    if (!pipe_ready()) return 0;
+    const int64_t nb_row = n_per_row / block_len(type), nb_mat = nrow * nb_row, rows = nmat * nrow;
+    const int64_t row_out = nb_row * (int64_t)gpuq_block_bytes(type);
+    // at least four chunks once the input passes 16 MiB, so that even one matrix overlaps its copies and kernels
+    const int64_t budget = std::min(stage_bytes(), std::max<int64_t>((int64_t)4 << 20, (rows * row_src + 3) / 4));
+    const int64_t chunk_rows = nrow * row_src <= budget ? nrow * std::max<int64_t>(1, budget / (nrow * row_src))
+                                                        : std::max<int64_t>(1, budget / row_src);
+    const int64_t max_rows = std::min(chunk_rows, rows);
+    const bool decode = !fused_src(src);
+    for (Slot &s : g_slot) {
+        if (!s.in.grow((size_t)(max_rows * row_src) + 16) || !s.out.grow((size_t)(max_rows * row_out) + 16) ||
+            !s.pin_in.grow((size_t)(max_rows * row_src)) || !s.pin_out.grow((size_t)(max_rows * row_out)))
+            return 0;
+        if (decode && !s.f32.grow((size_t)(max_rows * n_per_row * 4))) return 0;
+        s.used = false;
+    }
     const float *qw = nullptr;
     if (imatrix && type != T_Q8_0) {
         if (!g_qw.grow((size_t)nmat * n_per_row * 4)) return 0;
         if (hipMemcpy(g_qw.p, imatrix, (size_t)nmat * n_per_row * 4, hipMemcpyHostToDevice) != hipSuccess) return 0;
         qw = (const float *)g_qw.p;
     }
-    const void *qsrc = g_raw.p;
-    int qsrc_type = src;
-    if (!fused_src(src)) {
-        if (!g_f32.grow((size_t)n * 4) || !launch_decode(src, g_raw.p, (float *)g_f32.p, n, 0)) return 0;
-        qsrc = g_f32.p;
-        qsrc_type = T_F32;
+    if (hipMemsetAsync(g_err, 0, sizeof(int), g_st_q) != hipSuccess) return 0;
+
+    bool ok = true;
+    int64_t r0 = 0;
+    int i = 0;
+    auto drain = [&](int chunk) {   // the chunk's blocks: pinned -> dst
+        const Slot &s = g_slot[chunk % NSLOT];
+        if (hipEventSynchronize(s.returned) != hipSuccess) return false;
+        par_copy((uint8_t *)dst + s.r0 * row_out, s.pin_out.p, (size_t)(s.rows * row_out));
+        return true;
+    };
+    while (ok && r0 < rows) {
+        int64_t r1 = std::min(rows, r0 + chunk_rows);
+        if (chunk_rows < nrow) r1 = std::min(r1, (r0 / nrow + 1) * nrow);   // rows of one matrix
+        const int64_t cr = r1 - r0;
+        const size_t in_bytes = (size_t)(cr * row_src), out_bytes = (size_t)(cr * row_out);
+        Slot &s = g_slot[i % NSLOT];
+        // source bytes -> pinned, once the slot's previous H2D copy has read them; -> device, once the slot's
+        // previous kernels have read its device buffers
+        if (s.used && hipEventSynchronize(s.copied) != hipSuccess) { ok = false; break; }
+        par_copy(s.pin_in.p, (const uint8_t *)raw + r0 * row_src, in_bytes);
+        if (s.used) ok = hipStreamWaitEvent(g_st_in, s.quantized, 0) == hipSuccess;
+        ok = ok && hipMemcpyAsync(s.in.p, s.pin_in.p, in_bytes, hipMemcpyHostToDevice, g_st_in) == hipSuccess &&
+             hipEventRecord(s.copied, g_st_in) == hipSuccess;
+        // decode and quantize, once the bytes are in and the slot's previous blocks have left
+        ok = ok && hipStreamWaitEvent(g_st_q, s.copied, 0) == hipSuccess;
+        if (ok && s.used) ok = hipStreamWaitEvent(g_st_q, s.returned, 0) == hipSuccess;
+        const void *qsrc = decode ? s.f32.p : s.in.p;
+        if (ok && decode) ok = launch_decode(src, s.in.p, (float *)s.f32.p, cr * n_per_row, g_st_q);
+        if (ok) {
+            const float *cqw = qw ? qw + (r0 / nrow) * n_per_row : nullptr;
+            const QParams p = params_for(type, qsrc, s.out.p, cr * nb_row, cqw, nb_mat, nb_row, 1);
+            ok = dispatch(type, decode ? T_F32 : src, p, g_st_q) && hipEventRecord(s.quantized, g_st_q) == hipSuccess;
+        }
+        // blocks -> pinned (the slot's previous blocks were taken out of pin_out by the last iteration)
+        ok = ok && hipStreamWaitEvent(g_st_out, s.quantized, 0) == hipSuccess &&
+             hipMemcpyAsync(s.pin_out.p, s.out.p, out_bytes, hipMemcpyDeviceToHost, g_st_out) == hipSuccess &&
+             hipEventRecord(s.returned, g_st_out) == hipSuccess;
+        s.used = true;
+        s.r0 = r0;
+        s.rows = cr;
+        if (ok && i >= NSLOT - 1) ok = drain(i - (NSLOT - 1));   // frees the pinned blocks of the slot used next
+        r0 = r1;
+        ++i;
     }
-    if (hipMemsetAsync(g_err, 0, sizeof(int), 0) != hipSuccess) return 0;
-    const QParams p = params_for(type, qsrc, g_out.p, nunits, qw, nb_mat, nb_row, 1);
-    if (!dispatch(type, qsrc_type, p, 0)) return 0;
-    if (hipDeviceSynchronize() != hipSuccess) return 0;
+    for (int c = std::max(0, i - (NSLOT - 1)); ok && c < i; ++c) ok = drain(c);
+    // every stream is idle before the call returns (the buffers are reused by the next call)
+    bool idle = true;
+    for (hipStream_t st : {g_st_in, g_st_q, g_st_out}) idle = hipStreamSynchronize(st) == hipSuccess && idle;
+    if (!ok || !idle) return 0;
     int err = 0;
     if (hipMemcpy(&err, g_err, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess || err) return 0;
-    if (hipMemcpy(dst, g_out.p, out_bytes, hipMemcpyDeviceToHost) != hipSuccess) return 0;
-    return out_bytes;
+    return (size_t)(rows * row_out);
 }
 
 // the LDLQ loop's side stream and its events (created once, on the library's device; default priority)
