@@ -23,15 +23,17 @@
 #pragma once
 #include "frame.cuh"
 
-// per-wave LDS workspace of the search with M lists a lane (list e = lane*M + m). The owner values are staged a
-// lane (PL = false: the lane's M lists search for one group) or a list (PL = true: M groups of the lane), SW floats
-// each: NV x's then NV weights (SW = 2 NV).
+// per-wave LDS workspace of the search with M lists a lane. List m of lane L has the id e = m*64 + L (the search
+// order is lane by lane, list by list; the ids are laid out list-major so that the 64 lanes' writes of one list's
+// fields hit consecutive addresses). The owner values are staged a lane (PL = false: the lane's M lists search for
+// one group; row L) or a list (PL = true: M groups of the lane; row e), SW floats each: NV x's then NV weights
+// (SW = 2 NV), stored as SW/4 planes of float4 so that the lanes' staging writes are consecutive too.
 template <int M, int SW = 16, bool PL = false> struct CoopWSM {
     static_assert(M == 1 || M == 2 || M == 4, "lists a lane: 1, 2 or 4");
     static_assert(SW == 8 || SW == 16, "staged values: 4 or 8 x's and weights");
     static constexpr int sw = SW;
     static constexpr bool per_list = PL;
-    float stage[PL ? 64 * M : 64][SW];
+    float4 stage[SW / 4][PL ? 64 * M : 64];
     int2 ent[64 * M];               // list e: first point's offset | length << 21, next list with candidates | e << 8
     float esc[64 * M];              // list e: its scale
     unsigned long long key[64 * M]; // list e: min of (distance bits << 32 | list position << 12 | grid index)
@@ -42,23 +44,22 @@ using CoopWS = CoopWSM<1>;
 static constexpr int COOP_WS_BYTES = (int)sizeof(CoopWS);
 
 // write this lane's values for the search: n values and n weights (slot: the lane, or with per-list staging the
-// lane's list lane*M + m)
+// id m*64 + lane of the lane's list m)
 template <int NV, class W> DEV void coop_stage(W &ws, const float *xv, const float *wv, int slot = -1) {
     static_assert(2 * NV <= W::sw, "staged row too small");
-    float4 *s = (float4 *)ws.stage[slot < 0 ? lane_id() : slot];
+    const int row = slot < 0 ? lane_id() : slot;
 #pragma unroll
     for (int i = 0; i < NV / 4; ++i) {
-        s[i] = make_float4(xv[4 * i], xv[4 * i + 1], xv[4 * i + 2], xv[4 * i + 3]);
-        s[NV / 4 + i] = make_float4(wv[4 * i], wv[4 * i + 1], wv[4 * i + 2], wv[4 * i + 3]);
+        ws.stage[i][row] = make_float4(xv[4 * i], xv[4 * i + 1], xv[4 * i + 2], xv[4 * i + 3]);
+        ws.stage[NV / 4 + i][row] = make_float4(wv[4 * i], wv[4 * i + 1], wv[4 * i + 2], wv[4 * i + 3]);
     }
 }
 
 // an owner's staged values into registers
 template <class W> DEV void coop_fetch(const W &ws, int owner, float (&st)[16]) {
-    const float4 *sp = (const float4 *)ws.stage[owner];
 #pragma unroll
     for (int i = 0; i < W::sw / 4; ++i) {
-        const float4 v = sp[i];
+        const float4 v = ws.stage[i][owner];
         st[4 * i] = v.x; st[4 * i + 1] = v.y; st[4 * i + 2] = v.z; st[4 * i + 3] = v.w;
     }
 }
@@ -90,7 +91,7 @@ DEV int wave_incl_scan(int v) {
 // ev.point(idx): grid point idx (< 4096) as stored; ev(st, scale, pt): its distance for the owner's staged values st
 // (16 floats).
 //
-// The wave's 64*M lists are concatenated lane by lane, list by list, so M searches of every lane share one set-up
+// The wave's 64*M lists are concatenated lane by lane, list by list (ids m*64 + lane), so M searches of every lane share one set-up
 // and one last, partly filled round. Rounds run in chunks of CH (8; fewer where lists are short): a first pass walks
 // the chunk's positions (list,
 // list position) and issues their list reads, a second reads their grid points, a third evaluates them, so a chunk's
@@ -102,7 +103,6 @@ DEV int wave_incl_scan(int v) {
 template <int M, int CH = 8, class Eval, int SW, bool PL>
 DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&scale)[M], const uint16_t *neigh,
                        int neigh_len, CoopWSM<M, SW, PL> &ws, const Eval &ev, int (&gi)[M]) {
-    constexpr int LM = PL ? 0 : (M == 4 ? 2 : M == 2 ? 1 : 0);    // list -> staged row: e >> LM
     constexpr int OFF_MASK = (1 << 21) - 1;
     // the lists through a buffer resource: 32-bit offsets, and reads past the table return 0 instead of faulting
     const __amdgpu_buffer_rsrc_t nrs = __builtin_amdgcn_make_buffer_rsrc((void *)neigh, 0, neigh_len * 2, 0x00020000);
@@ -120,10 +120,10 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
     int first = -1, last = -1;
 #pragma unroll
     for (int m = M - 1; m >= 0; --m)
-        if (cnt[m] > 0) first = lane * M + m;
+        if (cnt[m] > 0) first = m * 64 + lane;
 #pragma unroll
     for (int m = 0; m < M; ++m)
-        if (cnt[m] > 0) last = lane * M + m;
+        if (cnt[m] > 0) last = m * 64 + lane;
     const unsigned long long after = has & ~((2ull << lane) - 1);
     const int nfirst = __shfl(first, after ? __ffsll((long long)after) - 1 : lane);
     // the wave's last list (read here, in wave-uniform control flow: a lane read inside a branch may not have been
@@ -133,7 +133,7 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
         int carry = after ? nfirst : -1;                // (the wave's last list links to itself)
 #pragma unroll
         for (int m = M - 1; m >= 0; --m) {
-            const int e = lane * M + m;
+            const int e = m * 64 + lane;
             ws.ent[e] = make_int2((off[m] + 1) | (cnt[m] << 21), (carry < 0 ? e : carry) | (e << 8));
             ws.esc[e] = scale[m];
             ws.key[e] = ~0ull;
@@ -149,7 +149,7 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
             const int lf = div_small(start + R - 1, R);
             const int ll = div_small(start + cnt[m] - 1, R);
             for (int L = lf; L <= ll && L < 64; ++L)
-                ws.mark[L] = (lane * M + m) | (((int)__umul24((unsigned)L, (unsigned)R) - start) << 8);
+                ws.mark[L] = (m * 64 + lane) | (((int)__umul24((unsigned)L, (unsigned)R) - start) << 8);
             start += cnt[m];
         }
     }
@@ -173,7 +173,7 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
     float st[16], sc = ws.esc[o];
     unsigned bbits = ~0u;
     int bown = 0, bidx = 0;
-    coop_fetch(ws, o >> LM, st);
+    coop_fetch(ws, PL || M == 1 ? o : (o & 63), st);
     for (int r0 = 0; r0 < R; r0 += CH) {
         const int rend = R - r0 < CH ? R - r0 : CH;
         int own_j[CH], idx[CH];         // list | list position << 8; the candidate's grid index
@@ -202,7 +202,7 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
                 const int e = own_j[r] & 255;
                 if (e != cur) {
                     atomicMin(&ws.key[cur], ((unsigned long long)bbits << 32) | (unsigned)((bown >> 8) << 12 | bidx));
-                    if (LM == 0 || ((e ^ cur) >> LM)) coop_fetch(ws, e >> LM, st);
+                    if (PL || M == 1 || ((e ^ cur) & 63)) coop_fetch(ws, PL || M == 1 ? e : (e & 63), st);
                     cur = e;
                     bbits = ~0u;
                     sc = ws.esc[e];
@@ -221,7 +221,7 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
 #pragma unroll
     for (int m = 0; m < M; ++m) {
         if (cnt[m] > 0) {
-            const unsigned long long k = ws.key[lane * M + m];
+            const unsigned long long k = ws.key[m * 64 + lane];
             gi[m] = (unsigned)(k >> 32) >= 0x7f7fffffu ? -1 : (int)(k & 0xfffu);
         }
     }

@@ -318,7 +318,7 @@ using Iq16WS = CoopWSM<2, 16, true>;
 
 // the two groups' grid indices of every lane at one scale (all lanes call it together): a group with act[k] takes
 // the grid point of its key (id) if the key is on the grid, else the winner of its neighbour list (the distances at
-// `scale`), one wave-wide call for both groups (their values staged beforehand, list lane*2 + k). A search that
+// `scale`), one wave-wide call for both groups (their values staged beforehand, list k*64 + lane). A search that
 // accepts nothing flags the error (the reference traps) and yields index 0. Inactive groups get 0.
 template <int GRID>
 DEV void iq2_16_points(const bool (&act)[2], float id, float scale, const float (&xval)[16], const int32_t *map3,
@@ -372,7 +372,7 @@ DEV float iq2_16_search(const float (&x)[16], const float (&qv)[16], float sigma
     bool on_grid[2] = {true, true};
     // the two groups' values, staged once for all the trials and the final pass
 #pragma unroll
-    for (int k = 0; k < 2; ++k) coop_stage<8>(ws, xval + 8 * k, waux + 8 * k, lane_id() * 2 + k);
+    for (int k = 0; k < 2; ++k) coop_stage<8>(ws, xval + 8 * k, waux + 8 * k, k * 64 + lane_id());
     const bool act_live[2] = {live, live};
 #pragma unroll 1
     for (int is = -9; is <= 9; ++is) {

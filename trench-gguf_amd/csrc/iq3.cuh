@@ -94,7 +94,7 @@ DEV void iq3_points(const bool (&act)[8], float id, float scale, const float (&x
             cnt[m] = srch ? m3_cnt(mk[m]) : 0;
             off[m] = srch ? m3_off(mk[m]) : 0;
             sc[m] = scale;
-            if (srch) coop_stage<4>(ws, xval + 4 * k, waux + 4 * k, lane_id() * 4 + m);
+            if (srch) coop_stage<4>(ws, xval + 4 * k, waux + 4 * k, m * 64 + lane_id());
         }
         coop_search_m<4, IQ3_CH>(cnt, off, sc, p.neigh, p.neigh_len, ws, EvalIq4{grid}, gi);
 #pragma unroll

@@ -178,13 +178,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
         for (int j = 0; j < 8; ++j) Bs[buf][lk][le + 16 * j] = bv[j];
     };
-    load(0);
-    stash(0);
-    __syncthreads();
-    int buf = 0;
-    for (int k0 = 0; k0 < QK; k0 += LDLQ_BK) {
-        const bool more = k0 + LDLQ_BK < QK;
-        if (more) load(k0 + LDLQ_BK);       // the next chunk's global reads overlap this chunk's MFMAs
+    float wv[4][4][4];                      // the wave's W values (full tiles: read during the last chunk)
+    auto read_w = [&](int i0, int i1) {
+#pragma unroll
+        for (int i = i0; i < i1; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float *wr = W + (m * ne1 + row0 + wr0 + 16 * i + 4 * e + lane / 16) * ne0 + col0 + wc0 + lane % 16;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) wv[i][e][j] = wr[16 * j];
+            }
+    };
+    auto chunk = [&](int buf) {             // this wave's MFMAs over the staged k-chunk
 #pragma unroll
         for (int ks = 0; ks < LDLQ_BK; ks += 4) {
             const int kk = ks + lane / 16;
@@ -199,23 +204,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
                 for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[i], b[j], acc[i][j], 0, 0, 0);
         }
-        if (more) stash(buf ^ 1);           // (the other buffer was last read before the previous barrier)
+    };
+    load(0);
+    stash(0);
+    __syncthreads();
+    int buf = 0;
+    for (int k0 = 0; k0 + LDLQ_BK < QK; k0 += LDLQ_BK) {
+        load(k0 + LDLQ_BK);                 // the next chunk's global reads overlap this chunk's MFMAs
+        chunk(buf);
+        stash(buf ^ 1);                     // (the other buffer was last read before the previous barrier)
         __syncthreads();
         buf ^= 1;
     }
+    if (full) read_w(0, 1);                 // half the epilogue's reads overlap the last chunk's MFMAs (all of
+    chunk(buf);                             // them would not fit in the registers beside the accumulators)
+    if (full) read_w(1, 4);
     // epilogue: every W value of the wave's sub-tile is read before the first store (a store between the reads
     // would make each read wait for the one before it); a full tile runs unguarded, so the stores need no
     // per-element branches (and their waits no conservative counts)
-    float wv[4][4][4];
     if (full) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float *wr = W + (m * ne1 + row0 + wr0 + 16 * i + 4 * e + lane / 16) * ne0 + col0 + wc0 + lane % 16;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) wv[i][e][j] = wr[16 * j];
-            }
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
