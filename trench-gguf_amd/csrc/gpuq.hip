@@ -437,9 +437,9 @@ bool side_stream_ready() {
 // W -= Es . U[c0 .. c0+255][cb .. ce) for every matrix
 bool launch_update(float *W, const double *Es, const double *U, int64_t u_stride, int64_t nmat, int64_t ne1,
                    int64_t ne0, int64_t c0, int64_t cb, int64_t ce, hipStream_t st) {
-    const dim3 ug((unsigned)((ce - cb + LDLQ_TN - 1) / LDLQ_TN), (unsigned)((ne1 + LDLQ_TM - 1) / LDLQ_TM),
-                  (unsigned)nmat);
-    hipLaunchKernelGGL(k_ldlq_update, ug, dim3(256), 0, st, W, Es, U, u_stride, ne1, ne0, c0, cb, ce);
+    const int64_t nt = ((ce - cb + LDLQ_TN - 1) / LDLQ_TN) * ((ne1 + LDLQ_TM - 1) / LDLQ_TM) * nmat;
+    const unsigned grid = (unsigned)((nt + 7) / 8 * 8);   // (a multiple of the 8 XCDs; see ldlq_tile)
+    hipLaunchKernelGGL(k_ldlq_update, dim3(grid), dim3(256), 0, st, W, Es, U, u_stride, nmat, ne1, ne0, c0, cb, ce);
     return hipGetLastError() == hipSuccess;
 }
 

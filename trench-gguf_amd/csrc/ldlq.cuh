@@ -132,16 +132,36 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_
 // a chunk). A loader thread moves k row t/16, elements t%16 + 16j: 16 lanes read 128 contiguous bytes and write 16
 // consecutive LDS doubles; LDS rows are 144 doubles apart (1152 B = 128 mod 256), so the MFMA operand reads (4 k
 // rows x 16 consecutive doubles a wave) and the loader's writes fall in distinct banks.
+//
+// Tiles are numbered matrix by matrix, and within a matrix in groups of LDLQ_GM row tiles, rows fastest, so that the
+// workgroups running together share LDLQ_GM Es panels and as many U panels. The 1-D grid (padded to a multiple of
+// 8) is dealt to the 8 XCDs round-robin, so workgroup i takes tile (i % 8) * nper + i / 8: each XCD works through one
+// contiguous range of tiles and its L2 holds the panels they share (128 x 256 doubles each, 256 KB).
 #define LDLQ_LDS_ROW 144
+#define LDLQ_GM 8
+DEV bool ldlq_tile(int64_t ntr, int64_t ntc, int64_t nmat, int64_t &m, int64_t &tr, int64_t &tc) {
+    const int64_t nt = ntr * ntc * nmat, nper = (nt + 7) / 8;
+    const int64_t t = (int64_t)(blockIdx.x % 8) * nper + blockIdx.x / 8;
+    if (t >= nt) return false;
+    const int64_t per = ntr * ntc, u = t % per;
+    m = t / per;
+    const int64_t gsz = LDLQ_GM * ntc, g = u / gsz, r0 = g * LDLQ_GM;
+    const int64_t gm = ntr - r0 < LDLQ_GM ? ntr - r0 : LDLQ_GM;   // rows of this group
+    const int64_t v = u % gsz;
+    tr = r0 + v % gm;
+    tc = v / gm;
+    return true;
+}
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_ldlq_update(
-    float *__restrict__ W, const double *__restrict__ Es, const double *__restrict__ U, int64_t u_stride, int64_t ne1,
-    int64_t ne0, int64_t c0, int64_t cb, int64_t ce) {
+    float *__restrict__ W, const double *__restrict__ Es, const double *__restrict__ U, int64_t u_stride, int64_t nmat,
+    int64_t ne1, int64_t ne0, int64_t c0, int64_t cb, int64_t ce) {
     __shared__ __align__(16) double As[2][LDLQ_BK][LDLQ_LDS_ROW];
     __shared__ __align__(16) double Bs[2][LDLQ_BK][LDLQ_LDS_ROW];
-    const int64_t m = blockIdx.z;
-    const int64_t R = (int64_t)gridDim.z * ne1;
-    const int64_t row0 = (int64_t)blockIdx.y * LDLQ_TM;
-    const int64_t col0 = cb + (int64_t)blockIdx.x * LDLQ_TN;
+    int64_t m, tr, tc;
+    if (!ldlq_tile((ne1 + LDLQ_TM - 1) / LDLQ_TM, (ce - cb + LDLQ_TN - 1) / LDLQ_TN, nmat, m, tr, tc)) return;
+    const int64_t R = nmat * ne1;
+    const int64_t row0 = tr * LDLQ_TM;
+    const int64_t col0 = cb + tc * LDLQ_TN;
     const double *Um = U + m * u_stride;
     const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
     const int wr0 = (wave >> 1) * 64, wc0 = (wave & 1) * 64;   // the wave's 64 x 64 sub-tile
