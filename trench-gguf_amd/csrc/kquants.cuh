@@ -157,6 +157,62 @@ template <int N> DEV float sym_levels(int nmax, const float (&x)[N], Lv<N> &L, c
     return scale;
 }
 
+// sym_levels over a group's G values that every lane of the group holds (Q3_K's 16 sub-block scales): the 19
+// evaluations (the first iscale, then the trials is = -9..-1, 1..9) are dealt one a lane (lanes 0-2 take a second),
+// each computed exactly as the serial loop computes it; every lane then replays ggml's acceptance chain over them in
+// trial order from the owners' sums. Returns the scale; lvl = the level (0 .. 2 nmax - 1) of value g (own = x[g]), or
+// 0 when the values are all negligible (make_qx_quants, gpuq/gpuq.hip:75-112).
+template <int G>
+DEV float sym_levels_grp(int nmax, const float (&x)[G], const float (&wv)[G], float own, int g, int &lvl) {
+    float amax = 0, mx = 0;
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+        const float ax = fabsf(x[i]);
+        if (ax > amax) { amax = ax; mx = x[i]; }
+    }
+    lvl = 0;
+    if (amax < EPS_GROUP) return 0.f;
+    constexpr int NE = 19;                      // evaluation e: 0 the first iscale, then is = e - 10 (e <= 9) or e - 9
+    auto iscale_of = [&](int e) -> float {
+        if (e == 0) return -nmax / mx;
+        const int is = e <= 9 ? e - 10 : e - 9;
+        return -(nmax + 0.1f * is) / mx;
+    };
+    auto eval = [&](int e, float &sumlx, float &suml2) {
+        const float iscale = iscale_of(e);
+        sumlx = 0;
+        suml2 = 0;
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            const int l = imax(-nmax, imin(nmax - 1, nint(iscale * x[i])));
+            sumlx += wv[i] * x[i] * l;
+            suml2 += wv[i] * l * l;
+        }
+    };
+    // round 0: evaluation g; round 1: evaluation G + g (lanes g < NE - G; the others repeat evaluation G)
+    float sx0, s20, sx1, s21;
+    eval(g, sx0, s20);
+    eval(G + (g < NE - G ? g : 0), sx1, s21);
+    // an evaluation's scale and best as the chain would set them on accepting it (the first: unconditionally)
+    const float sc0 = g == 0 ? (s20 ? sx0 / s20 : 0.0f) : sx0 / s20, bt0 = sc0 * sx0;
+    const float sc1 = sx1 / s21, bt1 = sc1 * sx1;
+    float best = grp_bcast<G>(bt0, 0);
+    int win = 0;
+#pragma unroll
+    for (int e = 1; e < NE; ++e) {
+        const int src = e < G ? e : e - G;
+        const float sumlx = grp_bcast<G>(e < G ? sx0 : sx1, src);
+        const float suml2 = grp_bcast<G>(e < G ? s20 : s21, src);
+        const float bt = grp_bcast<G>(e < G ? bt0 : bt1, src);
+        const bool acc = suml2 > 0 && sumlx * sumlx > best * suml2;
+        best = acc ? bt : best;
+        win = acc ? e : win;
+    }
+    const float scw0 = grp_bcast<G>(sc0, win < G ? win : 0), scw1 = grp_bcast<G>(sc1, win < G ? 0 : win - G);
+    lvl = imax(-nmax, imin(nmax - 1, nint(iscale_of(win) * own))) + nmax;
+    return win < G ? scw0 : scw1;
+}
+
 // Q3_K without an imatrix: 3-bit levels then coordinate descent on x^2 weights (gpuq/gpuq.hip:1468-1508)
 template <int N> DEV float sym3_levels(int nmax, const float (&x)[N], Lv<N> &L) {
     float amax = 0, mx = 0;
@@ -403,12 +459,7 @@ struct KQ3K {
             float sc_all[G], sw_all[G];
             grp_gather<G>(scale, sc_all);
             grp_gather<G>(s, sw_all);
-            Lv<G> Lsv;
-            d16 = f2h(sym_levels<G>(32, sc_all, Lsv, sw_all));
-            Ls = 0;
-#pragma unroll
-            for (int j = 0; j < G; ++j)
-                if (j == g) Ls = (int)Lsv.get(j);
+            d16 = f2h(sym_levels_grp<G>(32, sc_all, sw_all, scale, g, Ls));
         }
         if (Ls >= 0) {
             if (g < 8) img_or8(img, boff + 96 + g, (uint32_t)(Ls & 0xF));
