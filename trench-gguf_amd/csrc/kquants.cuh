@@ -111,6 +111,85 @@ template <int N> DEV float qp_levels(int nmax, const float (&x)[N], Lv<N> &L, co
     return suml2 > 0.0f ? sumlx / suml2 : 0.0f;
 }
 
+// qp_levels over a group's G values that every lane of the group holds (the k-quants' sub-block scales and mins):
+// the 9 first-scale evaluations (the first iscale, then is = -4..-1, 1..4) are dealt over the lanes, each computed as
+// the serial loop computes it, and every lane replays the strict-less minimum over them in trial order; the levels
+// and the refinement passes that follow run on every lane as in qp_levels.
+template <int G> DEV float qp_levels_grp(int nmax, const float (&x)[G], Lv<G> &L, const float (&qw)[G], int g) {
+    float mx = 0;
+#pragma unroll
+    for (int i = 0; i < G; ++i) mx = fmax_sel(mx, x[i]);
+    if (mx < EPS_GROUP) {
+        L.clear();
+        return 0.f;
+    }
+    constexpr int NE = 9, NR = (NE + G - 1) / G;
+    auto iscale_of = [&](int e) -> float {
+        if (e == 0) return nmax / mx;
+        const int is = e <= 4 ? e - 5 : e - 4;
+        return (0.1f * is + nmax) / mx;
+    };
+    float mse_r[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        const int e = r * G + g < NE ? r * G + g : NE - 1;
+        const float iscale_e = iscale_of(e);
+        const float scale_e = 1 / iscale_e;
+        float mse = 0;
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            const int lr = nint(iscale_e * x[i]);
+            // (the first evaluation takes the level unclamped, through its uint8 store; the trials clamp it)
+            const float lf = e == 0 ? (float)(uint32_t)lr : (float)imin(nmax, lr);
+            const float diff = x[i] - scale_e * lf;
+            mse += qw[i] * diff * diff;
+        }
+        mse_r[r] = mse;
+    }
+    float best = grp_bcast<G>(mse_r[0], 0);
+    int win = 0;
+#pragma unroll
+    for (int e = 1; e < NE; ++e) {
+        const float m = grp_bcast<G>(mse_r[e / G], e % G);
+        win = m < best ? e : win;
+        best = m < best ? m : best;
+    }
+    const float iscale = iscale_of(win);
+    float sumlx = 0, suml2 = 0;
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+        const int l = imin(nmax, nint(iscale * x[i]));
+        L.put(i, (uint32_t)l);
+        sumlx += qw[i] * x[i] * l;
+        suml2 += qw[i] * l * l;
+    }
+    for (int pass = 0; pass < 5; ++pass) {
+        int changed = 0;
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            const float w = qw[i];
+            const int Li = (int)L.get(i);
+            float slx = sumlx - w * x[i] * Li;
+            float sl2 = suml2 - w * Li * Li;
+            if (slx > 0 && sl2 > 0) {
+                const int nl = imin(nmax, nint(x[i] * sl2 / slx));
+                if (nl != Li) {
+                    slx += w * x[i] * nl;
+                    sl2 += w * nl * nl;
+                    if (slx * slx * suml2 > sumlx * sumlx * sl2) {
+                        L.put(i, (uint32_t)nl);
+                        sumlx = slx;
+                        suml2 = sl2;
+                        ++changed;
+                    }
+                }
+            }
+        }
+        if (!changed) break;
+    }
+    return suml2 > 0.0f ? sumlx / suml2 : 0.0f;
+}
+
 // symmetric levels (l + nmax) in [0, 2 nmax), best of 19 trial scales, wv = the importance (qw, or x^2)
 // (gpuq/gpuq.hip:1427-1466)
 template <int N> DEV float sym_levels(int nmax, const float (&x)[N], Lv<N> &L, const float (&wv)[N]) {
@@ -394,8 +473,8 @@ struct KQ2K {
             grp_gather<G>(mn, mn_all);
             grp_gather<G>(sw, sw_all);
             Lv<G> Ls, Lm;
-            const float dm = qp_levels<G>(15, sc_all, Ls, sw_all);
-            const float mm = qp_levels<G>(15, mn_all, Lm, sw_all);
+            const float dm = qp_levels_grp<G>(15, sc_all, Ls, sw_all, g);
+            const float mm = qp_levels_grp<G>(15, mn_all, Lm, sw_all, g);
             d16 = f2h(dm);
             m16 = f2h(mm);
             scb = 0;
@@ -545,8 +624,8 @@ template <int NMAX> struct KQ45K {
             grp_gather<G>(mn, mn_all);
             grp_gather<G>(s, sw_all);
             Lv<G> Lsv, Lmv;
-            const float db = qp_levels<G>(63, sc_all, Lsv, sw_all);
-            const float mb = qp_levels<G>(63, mn_all, Lmv, sw_all);
+            const float db = qp_levels_grp<G>(63, sc_all, Lsv, sw_all, g);
+            const float mb = qp_levels_grp<G>(63, mn_all, Lmv, sw_all, g);
 #pragma unroll
             for (int j = 0; j < G; ++j) {
                 ls[j] = Lsv.get(j);
