@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """bench.py - throughput of the MI355X GGUF quantizer on the configured synthetic workloads.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-host] [--quick]
 
 One "step" is one pass of the quantizer over one workload tensor already resident in HBM (the device entry point
 gpuq_requantize_dev: source bytes decoded in registers, quantized, blocks written to HBM). The headline line is the
@@ -366,6 +366,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--quick", action="store_true", help="headline workload only")
+    ap.add_argument("--no-host", action="store_true",
+                    help="skip the host entry point timings (their chunked launches would mix into a kernel profile)")
     ap.add_argument("--experts", type=int, default=0, help="cap the expert count of the MoE workloads (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -396,9 +398,10 @@ def main():
     if "cpu_baseline" in head:
         line["cpu_baseline"] = head["cpu_baseline"]
     line["sample_identical_to_oracle"] = head["sample_identical_to_oracle"]
-    log("host entry point: Q4_K on %s" % c2.name)
-    line["host_api"] = {"note": "PCIe-inclusive, pageable host memory in and out; not the value",
-                        "Q4_K": host_api(torch, gq, gpuq, c2, gpuq.Q4_K, 1, out)}
+    if not args.no_host:
+        log("host entry point: Q4_K on %s" % c2.name)
+        line["host_api"] = {"note": "PCIe-inclusive, pageable host memory in and out; not the value",
+                            "Q4_K": host_api(torch, gq, gpuq, c2, gpuq.Q4_K, 1, out)}
     per = {}
     if not args.quick:
         ksteps = max(1, min(args.steps, 5))
@@ -442,8 +445,9 @@ def main():
             if "cpu_baseline" in e:
                 e["speedup_vs_cpu"] = round(e["value"] / e["cpu_baseline"]["value"], 1)
             per[name] = e
-            log("host entry point: %s on 16 experts" % name)
-            line["host_api"][name] = host_api(torch, gq, gpuq, c3, typ, min(16, c3.nmat), out_t)
+            if not args.no_host:
+                log("host entry point: %s on 16 experts" % name)
+                line["host_api"][name] = host_api(torch, gq, gpuq, c3, typ, min(16, c3.nmat), out_t)
             del out_t
         del c3
         torch.cuda.empty_cache()
