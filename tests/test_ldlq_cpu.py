@@ -1,6 +1,8 @@
 """LDLQ on the CPU: the host's prepare_hessian against its defining equations, and the oracle's fixed-order loop
 against the properties that pin it: no feedback is plain quantization; a diagonal factor feeds nothing forward; the
-first update equals E U_BB^-1 U_B,rest computed independently in float64 (to f32 rounding)."""
+first update equals E U_BB^-1 U_B,rest computed independently in float64 (to f32 rounding); and on the reference's
+correlated design (tools/test_ldlq.py:42-50) the feedback lowers the proxy loss (tools/ldlq.py:110-113) that it
+exists to lower, in sequential order with imatrix weights and in act order with Schur weights."""
 import numpy as np
 import pytest
 
@@ -64,3 +66,41 @@ def test_first_update_is_the_block_solve(oracle_lib):
     want = Wp[0][:, 256:] - upd
     assert np.allclose(Wout[0][:, 256:], want, rtol=0, atol=4 * np.spacing(np.abs(want).max()))
     assert not np.array_equal(Wout[0][:, 256:], Wp[0][:, 256:])
+
+
+def correlated_design(ne1=32, ne0=1024, seed=1):
+    rng = np.random.default_rng(seed)
+    n = 4 * ne0
+    A = rng.standard_normal((ne0, ne0)).astype(np.float32) * 0.2 + np.eye(ne0, dtype=np.float32)
+    X = rng.standard_normal((n, ne0)).astype(np.float32) @ A
+    X *= (1 + 3 * rng.random(ne0, dtype=np.float32))[None]
+    H = (X.T @ X).astype(np.float64)
+    imatrix = (np.diag(H) / n).astype(np.float32)
+    W = (rng.standard_normal((ne1, ne0)) * 0.05).astype(np.float32)
+    return H, n, imatrix, W
+
+
+def test_proxy_loss_closed_form():
+    rng = np.random.default_rng(0)
+    W = rng.standard_normal((3, 4))
+    Q = rng.standard_normal((3, 4))
+    X = rng.standard_normal((10, 4))
+    H = X.T @ X
+    # tr((W-Q) H (W-Q)^T) / n = ||X (W-Q)^T||_F^2 / n
+    assert np.isclose(ldlq.proxy_loss(W, Q, H, 10), np.sum((X @ (W - Q).T) ** 2) / 10, rtol=1e-12)
+    assert ldlq.proxy_loss(W, W, H, 10) == 0.0
+
+
+@pytest.mark.parametrize("typ", [22, 16], ids=["iq2_s", "iq2_xxs"])
+def test_feedback_lowers_the_proxy_loss(oracle_lib, typ):
+    H, n, im, W = correlated_design()
+    ne1, ne0 = W.shape
+    plain = oracle_lib.dequantize(typ, oracle_lib.quantize(typ, W, im), W.size).reshape(ne1, ne0)
+    lp = ldlq.proxy_loss(W, plain, H, n)
+    for order, mode in (("seq", "imatrix"), ("act", "schur")):
+        U, perm, diag_n, _ = ldlq.prepare_hessian(H, n, damp=0.01, order=order)
+        qw = ldlq.block_weights(mode, U=U, perm=perm, diag_n=diag_n, imatrix=im)[None]
+        q, _ = oracle_lib.ldlq(typ, W[None][:, :, perm], U, qw, ldlq.slot_order(perm), feedback=True)
+        fb = oracle_lib.dequantize(typ, q[0], W.size).reshape(ne1, ne0)
+        lf = ldlq.proxy_loss(W, fb, H, n)
+        assert lf < 0.95 * lp, (order, mode, lf, lp)

@@ -111,6 +111,13 @@ def block_weights(mode, U=None, perm=None, diag_n=None, imatrix=None, bs=QK_K):
     raise ValueError(mode)
 
 
+def proxy_loss(W, deq, H, n):
+    """tr((W - Q) H (W - Q)^T) / n, the calibration inputs' squared output error that the feedback lowers
+    (tools/ldlq.py:110-113): W and deq [ne1, ne0] in the original column order, H [ne0, ne0]"""
+    D = np.asarray(W, dtype=np.float64) - np.asarray(deq, dtype=np.float64)
+    return float(np.sum((D @ np.asarray(H, dtype=np.float64)) * D) / max(float(n), 1.0))
+
+
 def quantize_matrix_dev(gq, typ, W, U, perm, qw, feedback=True, u_per_matrix=False, stream=None):
     """W: torch f32 [B, ne1, ne0] on the device (original column order, left unchanged); U: torch f64 [ne0, ne0]
     (or [B, ne0, ne0] with u_per_matrix); perm: [ne0] numpy/long; qw: torch f32 [B, ne0] importances in permuted
