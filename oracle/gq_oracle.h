@@ -3,7 +3,7 @@
  * TEST INFRASTRUCTURE ONLY. This library restates, on the CPU and in plain C, the arithmetic of ggml's
  * ggml_quantize_chunk / to_float for the types the GPU library serves, following the reference implementation
  * gpuq/gpuq.hip (which restates ggml-quants.c). Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg
- * may load it, and only as the checker or as the timed CPU baseline; the product library never links it.
+ * may load it, and only to check results or as the timed CPU baseline; the product library never links it.
  *
  * Built with gcc -O2 -ffp-contract=off (no -march=native): no FMA contraction, SSE scalar fp32 with IEEE division and
  * square root and no flush-to-zero, the arithmetic of a GGML_NATIVE=OFF libggml-base.

@@ -7,7 +7,7 @@ the product). This script runs that library on one MI355X over a row subset of t
   - q_<type>_<im|noim>: the quantized bytes (gpuq_quantize, one call a matrix), every type and imatrix mode;
   - dq_<type>: sha256 of to_float (gpuq_dequantize_dev) of the i-quant bytes, as hex;
   - meta: sha256 of the inputs and of the tables file.
-Run on a GPU box from the repository root:  python tests/golden/make_ref_golden.py [out.npz]
+Run on a machine with an MI355X, from the repository root:  python tests/golden/make_ref_golden.py [out.npz]
 """
 import ctypes
 import hashlib

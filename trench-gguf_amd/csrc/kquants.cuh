@@ -268,7 +268,7 @@ DEV float sym_levels_grp(int nmax, const float (&x)[G], const float (&wv)[G], fl
             suml2 += wv[i] * l * l;
         }
     };
-    // round 0: evaluation g; round 1: evaluation G + g (lanes g < NE - G; the others repeat evaluation G)
+    // pass 0: evaluation g; pass 1: evaluation G + g (lanes g < NE - G; the others repeat evaluation G)
     float sx0, s20, sx1, s21;
     eval(g, sx0, s20);
     eval(G + (g < NE - G ? g : 0), sx1, s21);
