@@ -83,18 +83,25 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_
                 for (int tj = 0; tj < 2; ++tj)
 #pragma unroll
                     for (int e = 0; e < 4; ++e) acc[ti][tj][e] = T[16 * ti + 4 * e + lane / 16][16 * tj + lane % 16];
-            for (int k0 = 0; k0 < 32 * c; k0 += 4) {
-                const int k = k0 + lane / 16;
-                double a[4], b[2];
+            // k in steps of 16: the operands of four MFMA k-steps are read together, so one memory latency covers
+            // four steps (the MFMAs still run in ascending k)
+            for (int k0 = 0; k0 < 32 * c; k0 += 16) {
+                double a[4][4], b[4][2];
 #pragma unroll
-                for (int ti = 0; ti < 4; ++ti) a[ti] = -Es[k * R + arow[ti]];
+                for (int s = 0; s < 4; ++s) {
+                    const int k = k0 + 4 * s + lane / 16;
 #pragma unroll
-                for (int tj = 0; tj < 2; ++tj) b[tj] = Um[(c0 + k) * ne0 + cc + 16 * tj + lane % 16];
+                    for (int ti = 0; ti < 4; ++ti) a[s][ti] = -Es[k * R + arow[ti]];
 #pragma unroll
-                for (int ti = 0; ti < 4; ++ti)
+                    for (int tj = 0; tj < 2; ++tj) b[s][tj] = Um[(c0 + k) * ne0 + cc + 16 * tj + lane % 16];
+                }
 #pragma unroll
-                    for (int tj = 0; tj < 2; ++tj)
-                        acc[ti][tj] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[ti], b[tj], acc[ti][tj], 0, 0, 0);
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+                        for (int tj = 0; tj < 2; ++tj)
+                            acc[ti][tj] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[s][ti], b[s][tj], acc[ti][tj], 0, 0, 0);
             }
 #pragma unroll
             for (int ti = 0; ti < 4; ++ti)
