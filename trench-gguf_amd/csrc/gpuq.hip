@@ -351,9 +351,16 @@ size_t quantize_host(int src, const void *raw, int type, void *dst, int64_t nmat
     const int64_t row_out = nb_row * (int64_t)gpuq_block_bytes(type);
     // at least four chunks once the input passes 16 MiB, so that even one matrix overlaps its copies and kernels
     const int64_t budget = std::min(stage_bytes(), std::max<int64_t>((int64_t)4 << 20, (rows * row_src + 3) / 4));
-    const int64_t chunk_rows = nrow * row_src <= budget ? nrow * std::max<int64_t>(1, budget / (nrow * row_src))
-                                                        : std::max<int64_t>(1, budget / row_src);
-    const int64_t max_rows = std::min(chunk_rows, rows);
+    // chunk i from row r0: whole matrices when it starts at a matrix and its budget holds one, else rows up to the
+    // end of the current matrix (so a chunk's blocks map to imatrix rows as in one launch); the first two chunks get
+    // a quarter and a half of the budget, so the first kernel starts after a small copy
+    auto chunk_end = [&](int64_t r0, int i) {
+        const int64_t br = std::max<int64_t>(1, (i == 0 ? budget / 4 : i == 1 ? budget / 2 : budget) / row_src);
+        const int64_t r1 = r0 % nrow == 0 && br >= nrow ? r0 + br / nrow * nrow
+                                                        : std::min(r0 + br, (r0 / nrow + 1) * nrow);
+        return std::min(r1, rows);
+    };
+    const int64_t max_rows = std::min(rows, std::max<int64_t>(1, budget / row_src));
     const bool decode = !fused_src(src);
     for (Slot &s : g_slot) {
         if (!s.in.grow((size_t)(max_rows * row_src) + 16) || !s.out.grow((size_t)(max_rows * row_out) + 16) ||
@@ -380,9 +387,7 @@ size_t quantize_host(int src, const void *raw, int type, void *dst, int64_t nmat
         return true;
     };
     while (ok && r0 < rows) {
-        int64_t r1 = std::min(rows, r0 + chunk_rows);
-        if (chunk_rows < nrow) r1 = std::min(r1, (r0 / nrow + 1) * nrow);   // rows of one matrix
-        const int64_t cr = r1 - r0;
+        const int64_t r1 = chunk_end(r0, i), cr = r1 - r0;
         const size_t in_bytes = (size_t)(cr * row_src), out_bytes = (size_t)(cr * row_out);
         Slot &s = g_slot[i % NSLOT];
         // source bytes -> pinned, once the slot's previous H2D copy has read them; -> device, once the slot's
