@@ -1,5 +1,6 @@
 """The host entry points' streamed pipeline: an input cut into chunks of whole matrices, or of rows of one matrix,
-that run through two slots (copy in / quantize / copy out overlapped) gives the bytes of the oracle over the whole
+that run through three slots (copy in / quantize / copy out overlapped; the first two chunks a quarter and a half of
+the budget) gives the bytes of the oracle over the whole
 input, matrix by matrix with each matrix's own imatrix row (gpuq/gpuq.hip:2219-2250 of the reference: the batch
 entry points take nmat matrices and nmat imatrix rows). GPUQ_STAGE_MB sets the chunk size; it is read on each call.
 """
@@ -56,8 +57,9 @@ def source_bytes(oracle_lib, src, x):
     return oracle_lib.quantize(8, x.reshape(-1, x.shape[-1])).reshape(-1)
 
 
-# (nmat, nrow, ncol, GPUQ_STAGE_MB): whole-matrix chunks (2 matrices a chunk, last chunk short), rows of one
-# matrix (a 2.5 MiB BF16 matrix in 1 MiB chunks: 256 + 256 + 128 rows), and one chunk holding everything
+# (nmat, nrow, ncol, GPUQ_STAGE_MB): whole-matrix chunks after two partial ones (0.5 MiB matrices, 1 MiB budget),
+# rows of one matrix (a 2.5 MiB BF16 matrix in chunks of at most 1 MiB, ending at the matrix), and an input small
+# enough for whole-matrix chunks after the first partial ones
 SHAPES = [(5, 128, 2048, 1), (2, 640, 2048, 1), (3, 64, 2048, 64)]
 
 
@@ -114,3 +116,33 @@ def test_stream_rejects_bad_shapes(gq):
     assert gq.gpuq_quantize(Q4_K, x.ctypes.data, out.ctypes.data, 0, 256, None) == 0
     assert gq.gpuq_quantize(Q4_K, x.ctypes.data, out.ctypes.data, 4, 100, None) == 0
     assert gq.gpuq_quantize(IQ2_XXS, x.ctypes.data, out.ctypes.data, 4, 256, None) == 0   # needs an imatrix
+
+
+def test_stream_concurrent_callers(gq, oracle_lib, stage_mb):
+    """host calls from two threads at once (ctypes drops the GIL) serialize on the library's lock: each gets its
+    own input's bytes (the reference's drivers hold a lock of their own, requant_experts.py:361)"""
+    import threading
+    stage_mb(1)
+    jobs = []
+    for seed in (11, 12):
+        x, im = matrices(2, 256, 2048, seed=seed)
+        raw = np.ascontiguousarray(source_bytes(oracle_lib, BF16, x))
+        f = oracle_lib.decode_src(BF16, raw, x.size).reshape(x.shape)
+        want = np.concatenate([oracle_lib.quantize(IQ2_XXS, f[m], im[m]).reshape(-1) for m in range(2)])
+        jobs.append((raw, im, want, np.zeros_like(want)))
+    got = [0, 0]
+
+    def run(k):
+        raw, im, _, out = jobs[k]
+        for _ in range(3):
+            got[k] = gq.gpuq_requantize_batch(BF16, raw.ctypes.data, IQ2_XXS, out.ctypes.data, 2, 256, 2048,
+                                              im.ctypes.data)
+    print("case stream concurrent callers", flush=True)
+    th = [threading.Thread(target=run, args=(k,)) for k in range(2)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    for k in range(2):
+        assert got[k] == jobs[k][2].size
+        assert np.array_equal(jobs[k][3], jobs[k][2])
