@@ -1,7 +1,6 @@
 """The host entry points' streamed pipeline: an input cut into chunks of whole matrices, or of rows of one matrix,
 that run through three slots (copy in / quantize / copy out overlapped; the first two chunks a quarter and a half of
-the budget) gives the bytes of the oracle over the whole
-input, matrix by matrix with each matrix's own imatrix row (gpuq/gpuq.hip:2219-2250 of the reference: the batch
+the budget) gives the bytes of the oracle over the whole input, matrix by matrix with each matrix's own imatrix row (gpuq/gpuq.hip:2219-2250 of the reference: the batch
 entry points take nmat matrices and nmat imatrix rows). GPUQ_STAGE_MB sets the chunk size; it is read on each call.
 """
 import os
@@ -58,8 +57,8 @@ def source_bytes(oracle_lib, src, x):
 
 
 # (nmat, nrow, ncol, GPUQ_STAGE_MB): whole-matrix chunks after two partial ones (0.5 MiB matrices, 1 MiB budget),
-# rows of one matrix (a 2.5 MiB BF16 matrix in chunks of at most 1 MiB, ending at the matrix), and an input small
-# enough for whole-matrix chunks after the first partial ones
+# rows of one matrix (a 2.5 MiB BF16 matrix in chunks of at most 1 MiB, ending at the matrix), and an input that
+# fits one chunk
 SHAPES = [(5, 128, 2048, 1), (2, 640, 2048, 1), (3, 64, 2048, 64)]
 
 
