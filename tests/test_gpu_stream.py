@@ -1,7 +1,8 @@
 """The host entry points' streamed pipeline: an input cut into chunks of whole matrices, or of rows of one matrix,
 that run through three slots (copy in / quantize / copy out overlapped; the first two chunks a quarter and a half of
-the budget) gives the bytes of the oracle over the whole input, matrix by matrix with each matrix's own imatrix row (gpuq/gpuq.hip:2219-2250 of the reference: the batch
-entry points take nmat matrices and nmat imatrix rows). GPUQ_STAGE_MB sets the chunk size; it is read on each call.
+the budget) gives the bytes of the oracle over the whole input, matrix by matrix with each matrix's own imatrix row
+(gpuq/gpuq.hip:2219-2250 of the reference: the batch entry points take nmat matrices and nmat imatrix rows).
+GPUQ_STAGE_MB sets the chunk size; it is read on each call.
 """
 import os
 
