@@ -88,6 +88,26 @@ size_t gpuq_requantize_dev(int src_type, const void *d_raw, int type, void *d_ds
 size_t gpuq_ldlq_dev(int type, float *d_wp, const double *d_u, int64_t u_stride, const float *d_qw, int64_t nmat,
                      int64_t ne1, int64_t ne0, const int64_t *blk_order, int feedback, void *d_out, void *stream);
 
+/* The LDLQ factor built on the device, replacing prepare_hessian / prepare_hessian_torch (tools/ldlq.py:34-68,
+ * 275-323), whose factorizations run in numpy or torch: d_H [ne0][ne0] f64 (device, row-major, the sum of x x^T over
+ * n inputs; not modified) -> d_U [ne0][ne0] f64 (device, row-major upper factor: U^T U = the inverse of the damped,
+ * normalized, block-permuted Hessian, with the reference's dead-column rule and its one retry with 10x more ridge),
+ * perm [ne0] (host: the column permutation, whole 256-column blocks; order 0 'seq', 1 'act'), diag_n [ne0] (host,
+ * diag(H)/n permuted; may be NULL) and dead [ne0] (host flags, original order; may be NULL). Uses rocSOLVER's potrf /
+ * potri (loaded on first use). Returns 0; 1 bad arguments (ne0 a multiple of 256, at most 65280), 2 rocBLAS or
+ * rocSOLVER not loadable, 3 not positive definite, 4 a HIP error. Synchronizes `stream`. */
+int gpuq_prepare_hessian_dev(const double *d_H, int64_t ne0, double n, double damp, int order, double *d_U,
+                             int64_t *perm, double *diag_n, unsigned char *dead, void *stream);
+
+/* The LDLQ loop from host memory, with no framework on the caller's side: the reference's tools/ldlq.py:71-107
+ * (quantize_matrix with weights = "imatrix") with the factor of gpuq_prepare_hessian_dev. W [nmat][ne1][ne0] f32
+ * (original column order, not modified), H [ne0][ne0] f64 shared by all matrices (h_stride 0) or one a matrix
+ * (h_stride ne0*ne0), n and damp and order as gpuq_prepare_hessian_dev, imatrix [nmat][ne0] (NULL only for a type that
+ * takes none). Writes every matrix's GGUF bytes to dst (blocks in their original slots) and returns their count, or 0
+ * on an error. Serializes on an internal lock; synchronous. */
+size_t gpuq_ldlq(int type, const float *W, const double *H, int64_t h_stride, double n, double damp, int order,
+                 const float *imatrix, int64_t nmat, int64_t ne1, int64_t ne0, void *dst);
+
 /* Reads and clears the flag the kernels set where the reference would trap (a key with no candidate point: non-
  * finite input or an inconsistent table). Synchronizes the device. */
 int gpuq_take_error(void);

@@ -80,3 +80,80 @@ def test_ldlq_without_feedback_is_plain_quantization(env, oracle_lib):
     for m in range(2):
         want = oracle_lib.quantize(16, W[m], imatrix)            # one whole-row call, tools/test_ldlq.py:69-73
         assert np.array_equal(got[m].cpu().numpy(), want)
+
+
+def prepare_dev(torch, gq, H, n, order, damp=0.01):
+    ne0 = H.shape[0]
+    dH = torch.from_numpy(np.ascontiguousarray(H, dtype=np.float64)).cuda()
+    dU = torch.empty_like(dH)
+    perm = np.empty(ne0, dtype=np.int64)
+    diag_n = np.empty(ne0, dtype=np.float64)
+    dead = np.empty(ne0, dtype=np.uint8)
+    rc = gq.gpuq_prepare_hessian_dev(dH.data_ptr(), ne0, float(n), damp, 1 if order == "act" else 0, dU.data_ptr(),
+                                     perm.ctypes.data, diag_n.ctypes.data, dead.ctypes.data,
+                                     torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, rc
+    return dU.cpu().numpy(), perm, diag_n, dead.astype(bool)
+
+
+@pytest.mark.parametrize("order", ["seq", "act"])
+def test_prepare_hessian_dev_matches_host(env, order):
+    """the device factor (rocSOLVER potrf / potri) against the host restatement of tools/ldlq.py:34-68: the same
+    permutation, diag and dead columns exactly, the same U to rounding, and U^T U = (Hp + ridge)^-1"""
+    torch, gpuq, gq = env
+    from gpuq import ldlq
+    H, n, _, _ = design(ne1=8, ne0=1024)
+    Hd = H.copy()
+    Hd[5, :] = 0                                           # a dead column (no energy), replaced by a unit row
+    Hd[:, 5] = 0
+    for Hx in (H, Hd):
+        U, perm, diag_n, dead = ldlq.prepare_hessian(Hx, n, damp=0.01, order=order)
+        print("case prepare_hessian_dev %s dead=%d" % (order, int(dead.sum())), flush=True)
+        Ud, pd, dd, zd = prepare_dev(torch, gq, Hx, n, order)
+        assert np.array_equal(pd, perm) and np.array_equal(zd, dead) and np.array_equal(dd, diag_n)
+        assert np.array_equal(np.tril(Ud, -1), np.zeros_like(Ud))
+        assert np.allclose(Ud, U, rtol=1e-6, atol=1e-9 * np.abs(U).max())
+        ne0 = Hx.shape[0]
+        Hn = Hx / n
+        Hn[dead, :] = 0
+        Hn[:, dead] = 0
+        Hn[dead, dead] = 1.0
+        Hp = Hn[np.ix_(perm, perm)]
+        Hp[np.diag_indices(ne0)] += 0.01 * np.mean(np.diag(Hp))
+        assert np.allclose(Ud.T @ Ud @ Hp, np.eye(ne0), atol=1e-8)
+
+
+@pytest.mark.parametrize("shared", [True, False], ids=["shared-H", "per-matrix-H"])
+@pytest.mark.parametrize("typ", [22, 16], ids=["iq2_s", "iq2_xxs"])
+def test_ldlq_host_matches_oracle(env, oracle_lib, typ, shared):
+    """gpuq_ldlq (host memory in and out, factor built on the device) == the oracle's loop on the same factor"""
+    torch, gpuq, gq = env
+    from gpuq import ldlq
+    H, n, imatrix, W = design(ne1=32, ne0=768)
+    H2, _, _, _ = design(ne1=32, ne0=768, seed=2)
+    Hs = [H, H] if shared else [H, H2]
+    ims = np.ascontiguousarray(np.stack([imatrix, imatrix * 0.5]).astype(np.float32))
+    want = []
+    for m in range(2):
+        U, perm, _, _ = prepare_dev(torch, gq, Hs[m], n, "act")
+        qw = ims[m][perm][None]
+        want.append(oracle_lib.ldlq(typ, W[m:m + 1][:, :, perm], U, qw, ldlq.slot_order(perm))[0][0])
+    want = np.stack(want)
+    out = np.zeros_like(want)
+    Hh = np.ascontiguousarray(H if shared else np.stack([H, H2]), dtype=np.float64)
+    print("case ldlq host %d shared=%s" % (typ, shared), flush=True)
+    got = gq.gpuq_ldlq(typ, np.ascontiguousarray(W).ctypes.data, Hh.ctypes.data, 0 if shared else 768 * 768,
+                       float(n), 0.01, 1, ims.ctypes.data, 2, 32, 768, out.ctypes.data)
+    assert got == out.nbytes
+    assert np.array_equal(out, want), "%d bytes differ" % int((out != want).sum())
+
+
+def test_quantize_matrix_host_wrapper(env, oracle_lib):
+    """the numpy wrapper over gpuq_ldlq: one imatrix row for all matrices, a 2-D W"""
+    torch, gpuq, gq = env
+    from gpuq import ldlq
+    H, n, imatrix, W = design(ne1=16, ne0=512)
+    got = ldlq.quantize_matrix_host(gq, 22, W[0], H, n, imatrix, order="seq")
+    U, perm, _, _ = prepare_dev(torch, gq, H, n, "seq")
+    want, _ = oracle_lib.ldlq(22, W[0:1][:, :, perm], U, imatrix[perm][None], ldlq.slot_order(perm))
+    assert np.array_equal(got, want)

@@ -4,7 +4,10 @@
 // The exported functions keep the reference library's signatures, return conventions and table file format
 // (gpuq/gpuq.hip:2059-2328 of the reference), so its Python drivers load this library unchanged; they are declared
 // with their reference counterparts in include/gpuq.h.
+#include <dlfcn.h>
 #include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
+#include <rocsolver/rocsolver.h>
 
 #include <cstdio>
 #include <cstring>
@@ -22,6 +25,7 @@
 #include "iq3.cuh"
 #include "dequant.cuh"
 #include "ldlq.cuh"
+#include "hessian.cuh"
 
 extern "C" size_t gpuq_block_bytes(int type);
 
@@ -733,4 +737,192 @@ extern "C" size_t gpuq_ldlq_dev(int type, float *d_wp, const double *d_u, int64_
             return 0;
     }
     return (size_t)(rows * nblk * bb);
+}
+
+// ------------------------------------------------------------------ the Hessian preparation and the host LDLQ loop
+namespace {
+
+// rocBLAS / rocSOLVER, opened on first use (the quantizer never needs them): the copies the process already loaded
+// when the caller's framework brought them (same sonames), else ROCm's
+struct Lapack {
+    bool tried = false, ok = false;
+    decltype(&rocblas_create_handle) create = nullptr;
+    decltype(&rocblas_set_stream) set_stream = nullptr;
+    decltype(&rocsolver_dpotrf) potrf = nullptr;
+    decltype(&rocsolver_dpotri) potri = nullptr;
+    rocblas_handle h = nullptr;
+};
+Lapack g_lp;
+std::mutex g_mu_h;   // the Hessian preparation's handle and buffers
+Buf g_hd;            // device: diag (f64) | perm (i64) | dead (u8) | factorization info
+
+bool lapack_ready() {
+    if (g_lp.tried) return g_lp.ok;
+    g_lp.tried = true;
+    void *blas = dlopen("librocblas.so.5", RTLD_NOW | RTLD_GLOBAL);
+    void *sol = dlopen("librocsolver.so.0", RTLD_NOW | RTLD_GLOBAL);
+    if (!blas || !sol) return false;
+    g_lp.create = (decltype(g_lp.create))dlsym(blas, "rocblas_create_handle");
+    g_lp.set_stream = (decltype(g_lp.set_stream))dlsym(blas, "rocblas_set_stream");
+    g_lp.potrf = (decltype(g_lp.potrf))dlsym(sol, "rocsolver_dpotrf");
+    g_lp.potri = (decltype(g_lp.potri))dlsym(sol, "rocsolver_dpotri");
+    if (!g_lp.create || !g_lp.set_stream || !g_lp.potrf || !g_lp.potri) return false;
+    if (hipSetDevice(g_device) != hipSuccess || g_lp.create(&g_lp.h) != rocblas_status_success) return false;
+    g_lp.ok = true;
+    return true;
+}
+
+// a factorization's info (0: done; > 0: not positive definite), -1 when it cannot be read
+int read_info(const int *d_info, hipStream_t st) {
+    int v = -1;
+    if (hipMemcpyAsync(&v, d_info, sizeof(int), hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess)
+        return -1;
+    return v;
+}
+
+std::mutex g_mu_l;   // the host LDLQ loop's buffers and stream
+Buf g_lH, g_lU, g_lW, g_lWp, g_lqw, g_lout, g_lperm;
+hipStream_t g_st_l = nullptr;
+
+}  // namespace
+
+// The LDLQ factor on the device: prepare_hessian (tools/ldlq.py:34-68 of the reference) on a device H [ne0][ne0]
+// (f64, row-major, symmetric: the sum of x x^T over n inputs). Writes d_U (row-major, upper: U^T U is the inverse of
+// Hp = Hn[perm][:, perm] + damp * mean(diag) * I, Hn = H / max(n, 1) with dead columns (diag <= 0) replaced by unit
+// rows; one retry with 10x more ridge when Hp does not factor), and on the host perm (ne0 column indices, whole
+// 256-blocks: order 0 'seq' keeps them in order, 1 'act' sorts them by descending energy, ties in order), diag_n
+// (diag(Hn)[perm]) and dead (ne0 flags, original order); either of the last two may be NULL. Returns 0, or 1 for bad
+// arguments, 2 when rocBLAS / rocSOLVER cannot be loaded, 3 when the matrix does not factor, 4 on a HIP error.
+extern "C" int gpuq_prepare_hessian_dev(const double *d_H, int64_t ne0, double n, double damp, int order, double *d_U,
+                                        int64_t *perm, double *diag_n, uint8_t *dead, void *stream) {
+    if (g_device < 0 || !d_H || !d_U || !perm || ne0 <= 0 || ne0 % QK || ne0 > 65535) return 1;   // (grid rows)
+    if ((order != 0 && order != 1) || !(damp >= 0) || ((uintptr_t)d_H & 7) || ((uintptr_t)d_U & 7)) return 1;
+    std::lock_guard<std::mutex> lock(g_mu_h);
+    if (!lapack_ready()) return 2;
+    const hipStream_t st = (hipStream_t)stream;
+    if (g_lp.set_stream(g_lp.h, st) != rocblas_status_success) return 4;
+    const size_t o_perm = (size_t)ne0 * 8, o_dead = o_perm + (size_t)ne0 * 8, o_info = (o_dead + ne0 + 15) & ~15ull;
+    if (!g_hd.grow(o_info + 16)) return 4;
+    double *dd = (double *)g_hd.p;
+    int64_t *dp = (int64_t *)((uint8_t *)g_hd.p + o_perm);
+    uint8_t *dz = (uint8_t *)g_hd.p + o_dead;
+    int *dinfo = (int *)((uint8_t *)g_hd.p + o_info);
+    const double nd = 1.0 > n ? 1.0 : n;                       // max(n, 1)
+    const unsigned g1 = (unsigned)((ne0 + 255) / 256);
+    const dim3 g2(g1, (unsigned)ne0);
+    hipLaunchKernelGGL(k_hess_diag, dim3(g1), dim3(256), 0, st, d_H, ne0, nd, dd);
+    std::vector<double> d((size_t)ne0);
+    if (hipMemcpyAsync(d.data(), dd, (size_t)ne0 * 8, hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess)
+        return 4;
+    std::vector<uint8_t> zd((size_t)ne0);
+    for (int64_t i = 0; i < ne0; ++i) {
+        zd[i] = d[i] <= 0;
+        if (zd[i]) d[i] = 1.0;
+    }
+    const int64_t nblk = ne0 / QK;
+    std::vector<int64_t> bo((size_t)nblk);
+    for (int64_t b = 0; b < nblk; ++b) bo[b] = b;
+    if (order == 1) {
+        std::vector<double> key((size_t)nblk);          // -energy; NaN sorts last, as numpy's argsort puts it
+        for (int64_t b = 0; b < nblk; ++b) {
+            double e = 0;
+            for (int i = 0; i < QK; ++i) e += d[b * QK + i];
+            key[b] = e != e ? HUGE_VAL : -e;
+        }
+        std::stable_sort(bo.begin(), bo.end(), [&](int64_t a, int64_t b) { return key[a] < key[b]; });
+    }
+    std::vector<int64_t> pm((size_t)ne0);
+    double mean = 0;
+    for (int64_t i = 0; i < ne0; ++i) {
+        pm[i] = bo[i / QK] * QK + i % QK;
+        mean += d[pm[i]];
+    }
+    mean /= (double)ne0;
+    if (hipMemcpyAsync(dp, pm.data(), (size_t)ne0 * 8, hipMemcpyHostToDevice, st) != hipSuccess ||
+        hipMemcpyAsync(dz, zd.data(), (size_t)ne0, hipMemcpyHostToDevice, st) != hipSuccess)
+        return 4;
+    const double r1 = damp * mean;
+    const rocblas_int nn = (rocblas_int)ne0;
+    hipLaunchKernelGGL(k_hess_perm, g2, dim3(256), 0, st, d_H, ne0, nd, (const int64_t *)dp, (const uint8_t *)dz, r1,
+                       d_U);
+    if (g_lp.potrf(g_lp.h, rocblas_fill_lower, nn, d_U, nn, dinfo) != rocblas_status_success) return 4;
+    int info = read_info(dinfo, st);
+    if (info > 0) {                                       // more ridge until it factors
+        hipLaunchKernelGGL(k_hess_perm, g2, dim3(256), 0, st, d_H, ne0, nd, (const int64_t *)dp,
+                           (const uint8_t *)dz, r1, d_U);
+        hipLaunchKernelGGL(k_diag_add, dim3(g1), dim3(256), 0, st, d_U, ne0, 10 * damp * mean);
+        if (g_lp.potrf(g_lp.h, rocblas_fill_lower, nn, d_U, nn, dinfo) != rocblas_status_success) return 4;
+        info = read_info(dinfo, st);
+    }
+    if (info != 0) return info > 0 ? 3 : 4;
+    // Hp^-1 from the factor (lower triangle), made symmetric, then its own lower factor: read row-major, U
+    if (g_lp.potri(g_lp.h, rocblas_fill_lower, nn, d_U, nn, dinfo) != rocblas_status_success) return 4;
+    if ((info = read_info(dinfo, st)) != 0) return info > 0 ? 3 : 4;
+    hipLaunchKernelGGL(k_sym_from_lower, g2, dim3(256), 0, st, d_U, ne0);
+    if (g_lp.potrf(g_lp.h, rocblas_fill_lower, nn, d_U, nn, dinfo) != rocblas_status_success) return 4;
+    if ((info = read_info(dinfo, st)) != 0) return info > 0 ? 3 : 4;
+    hipLaunchKernelGGL(k_zero_upper, g2, dim3(256), 0, st, d_U, ne0);
+    if (hipGetLastError() != hipSuccess || hipStreamSynchronize(st) != hipSuccess) return 4;
+    for (int64_t i = 0; i < ne0; ++i) {
+        perm[i] = pm[i];
+        if (diag_n) diag_n[i] = d[pm[i]];
+        if (dead) dead[i] = zd[i];
+    }
+    return 0;
+}
+
+// The LDLQ loop from host memory, with no framework on the caller's side (tools/ldlq.py:71-107 of the reference with
+// weights = "imatrix" and the factor from prepare_hessian): W [nmat][ne1][ne0] f32 (original column order), H the
+// Hessian sum over n inputs, [ne0][ne0] f64, one for all matrices (h_stride 0) or one a matrix (h_stride ne0*ne0),
+// imatrix [nmat][ne0] (NULL only for a type that takes none). Writes the GGUF bytes of every matrix to dst and returns
+// their count, or 0 on an error (a factor that cannot be built included).
+extern "C" size_t gpuq_ldlq(int type, const float *W, const double *H, int64_t h_stride, double n, double damp,
+                            int order, const float *imatrix, int64_t nmat, int64_t ne1, int64_t ne0, void *dst) {
+    if (!W || !H || !dst || nmat <= 0 || ne1 <= 0 || ne0 <= 0 || ne0 % QK) return 0;
+    if (h_stride != 0 && h_stride != ne0 * ne0) return 0;
+    if (!ldlq_type(type) || !gpuq_can_dequantize_type(type) || !type_ok(type, ne0, imatrix != nullptr)) return 0;
+    std::lock_guard<std::mutex> lock(g_mu_l);
+    if (!g_st_l && hipStreamCreateWithFlags(&g_st_l, hipStreamNonBlocking) != hipSuccess) return 0;
+    const hipStream_t st = g_st_l;
+    const int64_t nblk = ne0 / QK, row_bytes = nblk * (int64_t)gpuq_block_bytes(type);
+    const int64_t gsz = h_stride ? 1 : nmat;            // matrices that share a factor
+    const size_t wbytes = (size_t)gsz * ne1 * ne0 * 4, obytes = (size_t)gsz * ne1 * row_bytes;
+    if (!g_lH.grow((size_t)ne0 * ne0 * 8) || !g_lU.grow((size_t)ne0 * ne0 * 8) || !g_lW.grow(wbytes) ||
+        !g_lWp.grow(wbytes) || !g_lqw.grow((size_t)gsz * ne0 * 4) || !g_lout.grow(obytes + 16) ||
+        !g_lperm.grow((size_t)ne0 * 8))
+        return 0;
+    if (hipMemsetAsync(g_err, 0, sizeof(int), st) != hipSuccess) return 0;
+    std::vector<int64_t> perm((size_t)ne0), slots((size_t)nblk);
+    std::vector<float> qw(imatrix ? (size_t)gsz * ne0 : 0);
+    const unsigned gy = (unsigned)std::min<int64_t>(gsz * ne1, 65535);
+    for (int64_t m0 = 0; m0 < nmat; m0 += gsz) {
+        if (hipMemcpyAsync(g_lH.p, H + (h_stride ? m0 * h_stride : 0), (size_t)ne0 * ne0 * 8, hipMemcpyHostToDevice,
+                           st) != hipSuccess ||
+            gpuq_prepare_hessian_dev((const double *)g_lH.p, ne0, n, damp, order, (double *)g_lU.p, perm.data(),
+                                     nullptr, nullptr, st) != 0)
+            return 0;
+        for (int64_t k = 0; k < nblk; ++k) slots[k] = perm[k * QK] / QK;
+        for (int64_t m = 0; m < gsz && imatrix; ++m)
+            for (int64_t c = 0; c < ne0; ++c) qw[m * ne0 + c] = imatrix[(m0 + m) * ne0 + perm[c]];
+        if (hipMemcpyAsync(g_lW.p, W + m0 * ne1 * ne0, wbytes, hipMemcpyHostToDevice, st) != hipSuccess ||
+            hipMemcpyAsync(g_lperm.p, perm.data(), (size_t)ne0 * 8, hipMemcpyHostToDevice, st) != hipSuccess ||
+            (imatrix && hipMemcpyAsync(g_lqw.p, qw.data(), (size_t)gsz * ne0 * 4, hipMemcpyHostToDevice, st) !=
+                            hipSuccess))
+            return 0;
+        hipLaunchKernelGGL(k_gather_cols, dim3((unsigned)((ne0 + 255) / 256), gy), dim3(256), 0, st,
+                           (const float *)g_lW.p, (float *)g_lWp.p, (const int64_t *)g_lperm.p, gsz * ne1, ne0);
+        if (hipGetLastError() != hipSuccess) return 0;
+        if (!gpuq_ldlq_dev(type, (float *)g_lWp.p, (const double *)g_lU.p, 0, imatrix ? (const float *)g_lqw.p : nullptr,
+                           gsz, ne1, ne0, slots.data(), 1, g_lout.p, st))
+            return 0;
+        if (hipMemcpyAsync((uint8_t *)dst + m0 * ne1 * row_bytes, g_lout.p, obytes, hipMemcpyDeviceToHost, st) !=
+                hipSuccess ||
+            hipStreamSynchronize(st) != hipSuccess)
+            return 0;
+    }
+    int err = 0;
+    if (hipMemcpy(&err, g_err, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess || err) return 0;
+    return (size_t)(nmat * ne1 * row_bytes);
 }

@@ -138,3 +138,26 @@ def quantize_matrix_dev(gq, typ, W, U, perm, qw, feedback=True, u_per_matrix=Fal
     if got != out.numel():
         raise RuntimeError("gpuq_ldlq_dev failed (type %d, %d x %d x %d)" % (int(typ), B, ne1, ne0))
     return out
+
+
+def quantize_matrix_host(gq, typ, W, H, n, imatrix=None, damp=0.01, order="seq", h_per_matrix=False):
+    """The whole LDLQ path from numpy, no framework: W f32 [B, ne1, ne0] (original column order), H f64 [ne0, ne0]
+    (or [B, ne0, ne0] with h_per_matrix) the Hessian sum over n inputs, imatrix f32 [B, ne0] (or [ne0] for all).
+    The factor is built on the device (gpuq_prepare_hessian_dev) and the loop runs there (gpuq_ldlq_dev), weights =
+    the imatrix in the permuted order as tools/ldlq.py's default. Returns uint8 [B, ne1, nblk * block_bytes]."""
+    W = np.ascontiguousarray(W, dtype=np.float32)
+    if W.ndim == 2:
+        W = W[None]
+    B, ne1, ne0 = W.shape
+    H = np.ascontiguousarray(H, dtype=np.float64)
+    im = None
+    if imatrix is not None:
+        im = np.ascontiguousarray(np.broadcast_to(np.asarray(imatrix, dtype=np.float32), (B, ne0)))
+    tsize = gq.gpuq_block_bytes(int(typ))
+    out = np.empty((B, ne1, ne0 // QK_K * tsize), dtype=np.uint8)
+    got = gq.gpuq_ldlq(int(typ), W.ctypes.data, H.ctypes.data, ne0 * ne0 if h_per_matrix else 0, float(n), float(damp),
+                       1 if order == "act" else 0, None if im is None else im.ctypes.data, B, ne1, ne0,
+                       out.ctypes.data)
+    if got != out.nbytes:
+        raise RuntimeError("gpuq_ldlq failed (type %d, %d x %d x %d)" % (int(typ), B, ne1, ne0))
+    return out
