@@ -88,6 +88,12 @@ size_t gpuq_requantize_dev(int src_type, const void *d_raw, int type, void *d_ds
 size_t gpuq_ldlq_dev(int type, float *d_wp, const double *d_u, int64_t u_stride, const float *d_qw, int64_t nmat,
                      int64_t ne1, int64_t ne0, const int64_t *blk_order, int feedback, void *d_out, void *stream);
 
+/* H += X^T X on the device, replacing the float32-GEMM / float64-sum loop of tools/hessian_from_dump.py:73-79:
+ * d_X [nrows][ne0] f32, d_H [ne0][ne0] f64 (symmetric, kept symmetric), products exact in f64, sums over the rows in
+ * order on the f64 matrix cores. Asynchronous on `stream`. Returns 0; 1 bad arguments (ne0 a multiple of 256, at
+ * most 65280); 4 a HIP error. */
+int gpuq_hessian_accumulate_dev(const float *d_X, int64_t nrows, int64_t ne0, double *d_H, void *stream);
+
 /* The LDLQ factor built on the device, replacing prepare_hessian / prepare_hessian_torch (tools/ldlq.py:34-68,
  * 275-323), whose factorizations run in numpy or torch: d_H [ne0][ne0] f64 (device, row-major, the sum of x x^T over
  * n inputs; not modified) -> d_U [ne0][ne0] f64 (device, row-major upper factor: U^T U = the inverse of the damped,

@@ -157,3 +157,27 @@ def test_quantize_matrix_host_wrapper(env, oracle_lib):
     U, perm, _, _ = prepare_dev(torch, gq, H, n, "seq")
     want, _ = oracle_lib.ldlq(22, W[0:1][:, :, perm], U, imatrix[perm][None], ldlq.slot_order(perm))
     assert np.array_equal(got, want)
+
+
+def test_hessian_accumulate_dev(env):
+    """H += X^T X (tools/hessian_from_dump.py:73-79) on the f64 matrix cores: twice, onto a symmetric start, with a
+    row count that is not a multiple of the 16-row chunk; the result stays exactly symmetric"""
+    torch, gpuq, gq = env
+    rng = np.random.default_rng(4)
+    nrows, ne0 = 1000, 512
+    X = (rng.standard_normal((nrows, ne0)) * (1 + rng.random(ne0))).astype(np.float32)
+    A = rng.standard_normal((ne0, ne0))
+    H0 = A + A.T
+    dX = torch.from_numpy(X).cuda()
+    dH = torch.from_numpy(H0.copy()).cuda()
+    st = torch.cuda.current_stream().cuda_stream
+    print("case hessian_accumulate", flush=True)
+    for _ in range(2):
+        assert gq.gpuq_hessian_accumulate_dev(dX.data_ptr(), nrows, ne0, dH.data_ptr(), st) == 0
+    torch.cuda.synchronize()
+    H = dH.cpu().numpy()
+    Xd = X.astype(np.float64)
+    want = H0 + 2 * (Xd.T @ Xd)
+    assert np.array_equal(H, H.T)
+    assert np.allclose(H, want, rtol=1e-12, atol=1e-12 * np.abs(want).max())
+    assert gq.gpuq_hessian_accumulate_dev(dX.data_ptr(), nrows, 500, dH.data_ptr(), st) == 1

@@ -787,6 +787,20 @@ hipStream_t g_st_l = nullptr;
 
 }  // namespace
 
+// H += X^T X on the device (the Hessian sum of tools/hessian_from_dump.py:73-79 of the reference, there a float32
+// GEMM a chunk of rows added into float64): X [nrows][ne0] f32, H [ne0][ne0] f64 (symmetric, kept so); here every
+// product is exact in f64 and each sum runs over the rows in order on the f64 matrix cores. Asynchronous on stream.
+// Returns 0, 1 for bad arguments (ne0 a multiple of 256, at most 65280), 4 on a HIP error.
+extern "C" int gpuq_hessian_accumulate_dev(const float *d_X, int64_t nrows, int64_t ne0, double *d_H, void *stream) {
+    if (g_device < 0 || !d_X || !d_H || nrows <= 0 || ne0 <= 0 || ne0 % QK || ne0 > 65535) return 1;
+    if (((uintptr_t)d_X & 3) || ((uintptr_t)d_H & 7)) return 1;
+    const hipStream_t st = (hipStream_t)stream;
+    const unsigned nt = (unsigned)(ne0 / 128);
+    hipLaunchKernelGGL(k_xtx, dim3(nt, nt), dim3(256), 0, st, d_X, nrows, ne0, d_H);
+    hipLaunchKernelGGL(k_hess_mirror, dim3((unsigned)((ne0 + 255) / 256), (unsigned)ne0), dim3(256), 0, st, d_H, ne0);
+    return hipGetLastError() == hipSuccess ? 0 : 4;
+}
+
 // The LDLQ factor on the device: prepare_hessian (tools/ldlq.py:34-68 of the reference) on a device H [ne0][ne0]
 // (f64, row-major, symmetric: the sum of x x^T over n inputs). Writes d_U (row-major, upper: U^T U is the inverse of
 // Hp = Hn[perm][:, perm] + damp * mean(diag) * I, Hn = H / max(n, 1) with dead columns (diag <= 0) replaced by unit
