@@ -25,26 +25,31 @@
 
 // per-wave LDS workspace of the search with M lists a lane. List m of lane L has the id e = m*64 + L (the search
 // order is lane by lane, list by list; the ids are laid out list-major so that the 64 lanes' writes of one list's
-// fields hit consecutive addresses). The owner values are staged a lane (PL = false: the lane's M lists search for
-// one group; row L) or a list (PL = true: M groups of the lane; row e), SW floats each: NV x's then NV weights
-// (SW = 2 NV), stored as SW/4 planes of float4 so that the lanes' staging writes are consecutive too.
-template <int M, int SW = 16, bool PL = false> struct CoopWSM {
+// fields hit consecutive addresses). The owner values are staged in NP rows a lane, row e mod 64 NP for list e:
+// NP = 1 (PL = false) when the lane's M lists search for one group (row L), NP = M (PL = true) for M groups of the
+// lane (row e), or a divisor of M for M/NP searches of NP groups each (list m uses group m mod NP). A row holds SW
+// floats: NV x's then NV weights (SW = 2 NV), stored as SW/4 planes of float4 so that the lanes' staging writes are
+// consecutive too.
+template <int M, int SW = 16, bool PL = false, int NP = (PL ? M : 1)> struct CoopWSM {
     static_assert(M == 1 || M == 2 || M == 4, "lists a lane: 1, 2 or 4");
+    static_assert(NP >= 1 && NP <= M && M % NP == 0, "staged rows a lane: a divisor of M");
     static_assert(SW == 8 || SW == 16, "staged values: 4 or 8 x's and weights");
     static constexpr int sw = SW;
-    static constexpr bool per_list = PL;
-    float4 stage[SW / 4][PL ? 64 * M : 64];
+    static constexpr int np = NP;
+    float4 stage[SW / 4][64 * NP];
     int2 ent[64 * M];               // list e: first point's offset | length << 21, next list with candidates | e << 8
     float esc[64 * M];              // list e: its scale
     unsigned long long key[64 * M]; // list e: min of (distance bits << 32 | list position << 12 | grid index)
     int mark[64];                   // walker lane: the list of its first position | position in that list << 8
 };
-template <int M, int SW = 16, bool PL = false> constexpr int coop_wsm_bytes() { return (int)sizeof(CoopWSM<M, SW, PL>); }
+template <int M, int SW = 16, bool PL = false, int NP = (PL ? M : 1)> constexpr int coop_wsm_bytes() {
+    return (int)sizeof(CoopWSM<M, SW, PL, NP>);
+}
 using CoopWS = CoopWSM<1>;
 static constexpr int COOP_WS_BYTES = (int)sizeof(CoopWS);
 
-// write this lane's values for the search: n values and n weights (slot: the lane, or with per-list staging the
-// id m*64 + lane of the lane's list m)
+// write this lane's values for the search: n values and n weights (slot: the lane, or with several staged rows a
+// lane the row m*64 + lane of the lane's group m)
 template <int NV, class W> DEV void coop_stage(W &ws, const float *xv, const float *wv, int slot = -1) {
     static_assert(2 * NV <= W::sw, "staged row too small");
     const int row = slot < 0 ? lane_id() : slot;
@@ -100,9 +105,10 @@ DEV int wave_incl_scan(int v) {
 // to itself), so every slot holds a real candidate and needs no check: re-evaluating a candidate changes no minimum.
 // Along a walker's run a list's positions come in increasing order, so a strictly smaller distance alone keeps the
 // first of equal ones; the (distance, position) minimum across walkers is taken once per list visited.
-template <int M, int CH = 8, class Eval, int SW, bool PL>
+template <int M, int CH = 8, class Eval, int SW, bool PL, int NP>
 DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&scale)[M], const uint16_t *neigh,
-                       int neigh_len, CoopWSM<M, SW, PL> &ws, const Eval &ev, int (&gi)[M]) {
+                       int neigh_len, CoopWSM<M, SW, PL, NP> &ws, const Eval &ev, int (&gi)[M]) {
+    constexpr int ROWS = 64 * NP - 1;                   // list e's staged row: e & ROWS
     constexpr int OFF_MASK = (1 << 21) - 1;
     // the lists through a buffer resource: 32-bit offsets, and reads past the table return 0 instead of faulting
     const __amdgpu_buffer_rsrc_t nrs = __builtin_amdgcn_make_buffer_rsrc((void *)neigh, 0, neigh_len * 2, 0x00020000);
@@ -173,7 +179,7 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
     float st[16], sc = ws.esc[o];
     unsigned bbits = ~0u;
     int bown = 0, bidx = 0;
-    coop_fetch(ws, PL || M == 1 ? o : (o & 63), st);
+    coop_fetch(ws, o & ROWS, st);
     for (int r0 = 0; r0 < R; r0 += CH) {
         const int rend = R - r0 < CH ? R - r0 : CH;
         int own_j[CH], idx[CH];         // list | list position << 8; the candidate's grid index
@@ -202,7 +208,7 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
                 const int e = own_j[r] & 255;
                 if (e != cur) {
                     atomicMin(&ws.key[cur], ((unsigned long long)bbits << 32) | (unsigned)((bown >> 8) << 12 | bidx));
-                    if (PL || M == 1 || ((e ^ cur) & 63)) coop_fetch(ws, PL || M == 1 ? e : (e & 63), st);
+                    if (NP == M || ((e ^ cur) & ROWS)) coop_fetch(ws, e & ROWS, st);
                     cur = e;
                     bbits = ~0u;
                     sc = ws.esc[e];

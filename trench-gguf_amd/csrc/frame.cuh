@@ -117,14 +117,19 @@ template <class T, class = void> struct ws_of { static constexpr int v = 0; };
 template <class T> struct ws_of<T, decltype((void)T::WS)> { static constexpr int v = T::WS; };
 template <class T> constexpr int wave_bytes() { return img_bytes<T>() + ws_of<T>::v; }
 template <class T> DEV uint8_t *wave_ws(uint8_t *img) { return img + img_bytes<T>(); }
+// WGW (optional): waves a workgroup (default WG_WAVES), for types whose per-wave LDS would not let two workgroups
+// share a CU's LDS: one workgroup of twice the waves shares one copy of the tables
+template <class T, class = void> struct wgw_of { static constexpr int v = WG_WAVES; };
+template <class T> struct wgw_of<T, decltype((void)T::WGW)> { static constexpr int v = T::WGW; };
 // WPE (optional): the waves per SIMD the register allocation must allow (default 2)
 template <class T, class = void> struct wpe_of { static constexpr int v = 2; };
 template <class T> struct wpe_of<T, decltype((void)T::WPE)> { static constexpr int v = T::WPE; };
 
 template <class T, int SRC>
-__global__ __launch_bounds__(WG_THREADS) __attribute__((amdgpu_waves_per_eu(wpe_of<T>::v))) void k_quant(QParams p) {
+__global__ __launch_bounds__(64 * wgw_of<T>::v) __attribute__((amdgpu_waves_per_eu(wpe_of<T>::v))) void k_quant(
+    QParams p) {
     extern __shared__ __align__(16) uint8_t lds[];
-    constexpr int SPW = 64 / T::G;
+    constexpr int SPW = 64 / T::G, WGW = wgw_of<T>::v;
     if (T::TAB) {
         T::stage(p, lds);
         __syncthreads();
@@ -132,8 +137,8 @@ __global__ __launch_bounds__(WG_THREADS) __attribute__((amdgpu_waves_per_eu(wpe_
     const int wave = (int)(threadIdx.x >> 6), lane = lane_id();
     const int g = lane % T::G, slot = lane / T::G;
     uint8_t *img = lds + T::TAB + wave * wave_bytes<T>();
-    const int64_t nwaves = (int64_t)gridDim.x * WG_WAVES;
-    for (int64_t t = (int64_t)blockIdx.x * WG_WAVES + wave; t * SPW < p.nsb; t += nwaves) {
+    const int64_t nwaves = (int64_t)gridDim.x * WGW;
+    for (int64_t t = (int64_t)blockIdx.x * WGW + wave; t * SPW < p.nsb; t += nwaves) {
         const int64_t b0 = t * SPW;
         const int nact = (int)(p.nsb - b0 < SPW ? p.nsb - b0 : SPW);
         const int64_t b = b0 + (slot < nact ? slot : nact - 1);

@@ -133,14 +133,14 @@ template <class V> bool upload(V **dst, const std::vector<V> &src) {
 
 // ------------------------------------------------------------------ launch plumbing
 template <class T, int SRC> bool launch_q(const QParams &p, hipStream_t st) {
-    constexpr int spw = 64 / T::G;
+    constexpr int spw = 64 / T::G, wgw = wgw_of<T>::v;
     const int64_t tiles = (p.nsb + spw - 1) / spw;
-    int64_t wgs = (tiles + WG_WAVES - 1) / WG_WAVES;
-    const int64_t cap = (int64_t)g_ncu * 8;
+    int64_t wgs = (tiles + wgw - 1) / wgw;
+    const int64_t cap = (int64_t)g_ncu * 32 / wgw;          // 32 waves a CU in flight or queued
     if (wgs > cap) wgs = cap;
     if (wgs < 1) wgs = 1;
-    const size_t lds = (size_t)T::TAB + WG_WAVES * wave_bytes<T>();
-    hipLaunchKernelGGL((k_quant<T, SRC>), dim3((unsigned)wgs), dim3(WG_THREADS), lds, st, p);
+    const size_t lds = (size_t)T::TAB + wgw * wave_bytes<T>();
+    hipLaunchKernelGGL((k_quant<T, SRC>), dim3((unsigned)wgs), dim3(64 * wgw), lds, st, p);
     return hipGetLastError() == hipSuccess;
 }
 

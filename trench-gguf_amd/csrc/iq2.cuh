@@ -28,9 +28,9 @@ template <int GRID> struct Iq8Tab {
     static DEV void stage(const QParams &p, uint8_t *lds) {
         const uint4 *gs = (const uint4 *)p.grid;
         uint4 *gd = (uint4 *)lds;
-        for (int i = threadIdx.x; i < GRIDB / 16; i += WG_THREADS) gd[i] = gs[i];
+        for (int i = threadIdx.x; i < GRIDB / 16; i += blockDim.x) gd[i] = gs[i];
         int32_t *md = (int32_t *)(lds + GRIDB);
-        for (int i = threadIdx.x; i < NKEY3; i += WG_THREADS) md[i] = p.map3[i];
+        for (int i = threadIdx.x; i < NKEY3; i += blockDim.x) md[i] = p.map3[i];
     }
     static DEV const uint64_t *grid(const uint8_t *lds) { return (const uint64_t *)lds; }
     static DEV const int32_t *map3(const uint8_t *lds) { return (const int32_t *)(lds + GRIDB); }
@@ -313,35 +313,37 @@ struct KIQ2XXS : Iq8Tab<256> {
 // IQ2_S's one-shell neighbour lists are short (a few rounds a call): chunks of 2 rounds waste the least
 // (IQ2_XS's two-shell lists are longer: 8 rounds a chunk, measured 3% faster than 2)
 template <int GRID> constexpr int ch16() { return GRID == 512 ? 8 : 2; }
-// the search workspace of the 16-weight types: the lane's two groups as two lists, each with its staged values
-using Iq16WS = CoopWSM<2, 16, true>;
+// the search workspace of the 16-weight types: two trial scales of the lane's two groups as four lists (list
+// t*2 + k: trial t, group k), the two groups' values staged once (row k*64 + lane)
+using Iq16WS = CoopWSM<4, 16, true, 2>;
 
-// the two groups' grid indices of every lane at one scale (all lanes call it together): a group with act[k] takes
-// the grid point of its key (id) if the key is on the grid, else the winner of its neighbour list (the distances at
-// `scale`), one wave-wide call for both groups (their values staged beforehand, list k*64 + lane). A search that
-// accepts nothing flags the error (the reference traps) and yields index 0. Inactive groups get 0.
+// the two groups' grid indices of every lane at two scales (all lanes call it together): list m = t*2 + k with
+// act[m] takes the grid point of group k's key at id[t] if the key is on the grid, else the winner of its neighbour
+// list (the distances at scale[t]), one wave-wide call for the four lists (the groups' values staged beforehand). A
+// search that accepts nothing flags the error (the reference traps) and yields index 0. Inactive lists get 0.
 template <int GRID>
-DEV void iq2_16_points(const bool (&act)[2], float id, float scale, const float (&xval)[16], const int32_t *map3,
-                       const QParams &p, const uint64_t *grid, Iq16WS &ws, int (&gi)[2], bool (&og)[2]) {
-    int mk[2], cnt[2], off[2], g[2];
-    float sc[2];
+DEV void iq2_16_points(const bool (&act)[4], const float (&id)[2], const float (&scale)[2], const float (&xval)[16],
+                       const int32_t *map3, const QParams &p, const uint64_t *grid, Iq16WS &ws, int (&gi)[4],
+                       bool (&og)[4]) {
+    int mk[4], cnt[4], off[4], g[4];
+    float sc[4];
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        mk[k] = act[k] ? map3[group_key3(xval + 8 * k, id)] : 0;
-        og[k] = mk[k] >= 0;
-        cnt[k] = act[k] && mk[k] < 0 ? m3_cnt(mk[k]) : 0;
-        off[k] = act[k] && mk[k] < 0 ? m3_off(mk[k]) : 0;
-        sc[k] = scale;
+    for (int m = 0; m < 4; ++m) {
+        mk[m] = act[m] ? map3[group_key3(xval + 8 * (m & 1), id[m >> 1])] : 0;
+        og[m] = mk[m] >= 0;
+        cnt[m] = act[m] && mk[m] < 0 ? m3_cnt(mk[m]) : 0;
+        off[m] = act[m] && mk[m] < 0 ? m3_off(mk[m]) : 0;
+        sc[m] = scale[m >> 1];
     }
-    coop_search_m<2, ch16<GRID>()>(cnt, off, sc, p.neigh, p.neigh_len, ws, EvalIq8{grid}, g);
+    coop_search_m<4, ch16<GRID>()>(cnt, off, sc, p.neigh, p.neigh_len, ws, EvalIq8{grid}, g);
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        gi[k] = mk[k];
-        if (act[k] && mk[k] < 0) {
-            gi[k] = g[k];
-            if (g[k] < 0) {
+    for (int m = 0; m < 4; ++m) {
+        gi[m] = mk[m];
+        if (act[m] && mk[m] < 0) {
+            gi[m] = g[m];
+            if (g[m] < 0) {
                 flag_err(p);
-                gi[k] = 0;
+                gi[m] = 0;
             }
         }
     }
@@ -373,34 +375,43 @@ DEV float iq2_16_search(const float (&x)[16], const float (&qv)[16], float sigma
     // the two groups' values, staged once for all the trials and the final pass
 #pragma unroll
     for (int k = 0; k < 2; ++k) coop_stage<8>(ws, xval + 8 * k, waux + 8 * k, k * 64 + lane_id());
-    const bool act_live[2] = {live, live};
+    // the 19 trials two a call (the last call has one), accepted in trial order
 #pragma unroll 1
-    for (int is = -9; is <= 9; ++is) {
-        const float id = (5 + is * 0.1f) / mx;
-        const float this_scale = 1 / id;
-        int Pa[2];
-        bool og[2];
-        iq2_16_points<GRID>(act_live, id, this_scale, xval, map3, p, grid, ws, Pa, og);
-        float sumqx = 0, sumq2 = 0;
+    for (int is = -9; is <= 9; is += 2) {
+        const bool two = is < 9;                    // (wave-uniform)
+        float id[2], tsc[2];
+        id[0] = (5 + is * 0.1f) / mx;
+        id[1] = (5 + (is + 1) * 0.1f) / mx;
+        tsc[0] = 1 / id[0];
+        tsc[1] = 1 / id[1];
+        const bool act[4] = {live, live, live && two, live && two};
+        int Pa[4];
+        bool og[4];
+        iq2_16_points<GRID>(act, id, tsc, xval, map3, p, grid, ws, Pa, og);
 #pragma unroll
-        for (int k = 0; k < 2; ++k) sums_q8(weight + 8 * k, xval + 8 * k, grid[Pa[k]], sumqx, sumq2);
-        if (live && sumq2 > 0 && sumqx * sumqx > best * sumq2) {
-            scale = sumqx / sumq2;
-            best = scale * sumqx;
-            P[0] = Pa[0];
-            P[1] = Pa[1];
-            on_grid[0] = og[0];
-            on_grid[1] = og[1];
+        for (int t = 0; t < 2; ++t) {
+            if (t == 1 && !two) break;
+            float sumqx = 0, sumq2 = 0;
+#pragma unroll
+            for (int k = 0; k < 2; ++k) sums_q8(weight + 8 * k, xval + 8 * k, grid[Pa[2 * t + k]], sumqx, sumq2);
+            if (live && sumq2 > 0 && sumqx * sumqx > best * sumq2) {
+                scale = sumqx / sumq2;
+                best = scale * sumqx;
+                P[0] = Pa[2 * t];
+                P[1] = Pa[2 * t + 1];
+                on_grid[0] = og[2 * t];
+                on_grid[1] = og[2 * t + 1];
+            }
         }
     }
     // (a group left at levels 0 is on the grid: on_grid stays true for it)
     const bool fin = live && (!on_grid[0] || !on_grid[1]) && scale > 0;
     {
-        const float id = 1 / scale;
-        const bool act[2] = {fin && !on_grid[0], fin && !on_grid[1]};
-        int gi[2];
-        bool og[2];
-        iq2_16_points<GRID>(act, id, scale, xval, map3, p, grid, ws, gi, og);
+        const float id[2] = {1 / scale, 1 / scale}, fsc[2] = {scale, scale};
+        const bool act[4] = {fin && !on_grid[0], fin && !on_grid[1], false, false};
+        int gi[4];
+        bool og[4];
+        iq2_16_points<GRID>(act, id, fsc, xval, map3, p, grid, ws, gi, og);
         float sumqx = 0, sumq2 = 0;
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
@@ -428,7 +439,7 @@ DEV float iq2_16_search(const float (&x)[16], const float (&qv)[16], float sigma
 
 // IQ2_S: block d qs[64] (32 grid bytes, 32 sign bytes) qh[8] scales[8] (82 bytes); lane g = 16-weight sub-block g
 struct KIQ2S : Iq8Tab<1024> {
-    static constexpr int BS = QK, G = 16, N = 16, BB = 82, WS = coop_wsm_bytes<2, 16, true>();
+    static constexpr int BS = QK, G = 16, N = 16, BB = 82, WS = coop_wsm_bytes<4, 16, true, 2>(), WGW = 8;
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
                           const QParams &p) {
         float qv[N], sq[N];
@@ -462,7 +473,7 @@ struct KIQ2S : Iq8Tab<1024> {
 
 // IQ2_XS: block d qs[32] u16 scales[8] (74 bytes); qs[2g+k] = grid index | signs << 9
 struct KIQ2XS : Iq8Tab<512> {
-    static constexpr int BS = QK, G = 16, N = 16, BB = 74, WS = coop_wsm_bytes<2, 16, true>();
+    static constexpr int BS = QK, G = 16, N = 16, BB = 74, WS = coop_wsm_bytes<4, 16, true, 2>(), WGW = 8;
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
                           const QParams &p) {
         float qv[N], sq[N];

@@ -31,9 +31,9 @@ template <int GRID> struct Iq4Tab {
     static constexpr int TAB = (GRIDB + NKEY8 * 4 + 15) & ~15;
     static DEV void stage(const QParams &p, uint8_t *lds) {
         uint32_t *gd = (uint32_t *)lds;
-        for (int i = threadIdx.x; i < GRID; i += WG_THREADS) gd[i] = (uint32_t)p.grid[i];
+        for (int i = threadIdx.x; i < GRID; i += blockDim.x) gd[i] = (uint32_t)p.grid[i];
         int32_t *md = (int32_t *)(lds + GRIDB);
-        for (int i = threadIdx.x; i < NKEY8; i += WG_THREADS) md[i] = p.map3[i];
+        for (int i = threadIdx.x; i < NKEY8; i += blockDim.x) md[i] = p.map3[i];
     }
     static DEV const uint32_t *grid(const uint8_t *lds) { return (const uint32_t *)lds; }
     static DEV const int32_t *map(const uint8_t *lds) { return (const int32_t *)(lds + GRIDB); }
