@@ -101,11 +101,14 @@ DEV int wave_incl_scan(int v) {
 // the chunk's positions (list,
 // list position) and issues their list reads, a second reads their grid points, a third evaluates them, so a chunk's
 // reads are in flight together.
+// SLOTV: each slot's owner values and scale are read from LDS with its grid point, instead of once per list visited
+// into registers (for short lists, where a walker changes lists every few positions and the per-list read would
+// stall the evaluation that follows it).
 // A walker that has dealt with its own positions walks on through the following lists (the wave's last list links
 // to itself), so every slot holds a real candidate and needs no check: re-evaluating a candidate changes no minimum.
 // Along a walker's run a list's positions come in increasing order, so a strictly smaller distance alone keeps the
 // first of equal ones; the (distance, position) minimum across walkers is taken once per list visited.
-template <int M, int CH = 8, class Eval, int SW, bool PL, int NP>
+template <int M, int CH = 8, bool SLOTV = false, class Eval, int SW, bool PL, int NP>
 DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&scale)[M], const uint16_t *neigh,
                        int neigh_len, CoopWSM<M, SW, PL, NP> &ws, const Eval &ev, int (&gi)[M]) {
     constexpr int ROWS = 64 * NP - 1;                   // list e's staged row: e & ROWS
@@ -179,7 +182,7 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
     float st[16], sc = ws.esc[o];
     unsigned bbits = ~0u;
     int bown = 0, bidx = 0;
-    coop_fetch(ws, o & ROWS, st);
+    if (!SLOTV) coop_fetch(ws, o & ROWS, st);
     for (int r0 = 0; r0 < R; r0 += CH) {
         const int rend = R - r0 < CH ? R - r0 : CH;
         int own_j[CH], idx[CH];         // list | list position << 8; the candidate's grid index
@@ -202,18 +205,29 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
         }
 #pragma unroll
         for (int r = 0; r < CH; ++r) pt[r] = ev.point(idx[r]);
+        float sv[SLOTV ? CH : 1][16], ss[SLOTV ? CH : 1];
+        if (SLOTV) {
+#pragma unroll
+            for (int r = 0; r < CH; ++r) {
+                const int e = own_j[r] & 255;
+                coop_fetch(ws, e & ROWS, sv[r]);
+                ss[r] = ws.esc[e];
+            }
+        }
 #pragma unroll
         for (int r = 0; r < CH; ++r) {
             if (r < rend) {
                 const int e = own_j[r] & 255;
                 if (e != cur) {
                     atomicMin(&ws.key[cur], ((unsigned long long)bbits << 32) | (unsigned)((bown >> 8) << 12 | bidx));
-                    if (NP == M || ((e ^ cur) & ROWS)) coop_fetch(ws, e & ROWS, st);
+                    if (!SLOTV) {
+                        if (NP == M || ((e ^ cur) & ROWS)) coop_fetch(ws, e & ROWS, st);
+                        sc = ws.esc[e];
+                    }
                     cur = e;
                     bbits = ~0u;
-                    sc = ws.esc[e];
                 }
-                const unsigned b = __float_as_uint(ev(st, sc, pt[r]));
+                const unsigned b = __float_as_uint(SLOTV ? ev(sv[r], ss[r], pt[r]) : ev(st, sc, pt[r]));
                 const bool lt = b < bbits;              // (selects, not a branch)
                 bbits = lt ? b : bbits;
                 bown = lt ? own_j[r] : bown;

@@ -310,9 +310,10 @@ struct KIQ2XXS : Iq8Tab<256> {
 // ------------------------------------------------------------------ IQ2_XS / IQ2_S: the 16-weight search
 // (gpuq/gpuq.hip:690-822, 824-969). Returns the sub-block scale; gidx the two grid indices, bsg the two sign bytes;
 // live = false for a skipped (negligible) sub-block.
-// IQ2_S's one-shell neighbour lists are short (a few rounds a call): chunks of 2 rounds waste the least
-// (IQ2_XS's two-shell lists are longer: 8 rounds a chunk, measured 3% faster than 2)
-template <int GRID> constexpr int ch16() { return GRID == 512 ? 8 : 2; }
+// IQ2_S's one-shell neighbour lists are short (3.4 points on average): its searches read each slot's owner values
+// with the slot (SLOTV) in chunks of 4 rounds (3% faster than per-list reads in chunks of 2); IQ2_XS's two-shell
+// lists are longer: per-list reads, 8 rounds a chunk (measured 3% faster than 2)
+template <int GRID> constexpr int ch16() { return GRID == 512 ? 8 : 4; }
 // the search workspace of the 16-weight types: two trial scales of the lane's two groups as four lists (list
 // t*2 + k: trial t, group k), the two groups' values staged once (row k*64 + lane)
 using Iq16WS = CoopWSM<4, 16, true, 2>;
@@ -335,7 +336,7 @@ DEV void iq2_16_points(const bool (&act)[4], const float (&id)[2], const float (
         off[m] = act[m] && mk[m] < 0 ? m3_off(mk[m]) : 0;
         sc[m] = scale[m >> 1];
     }
-    coop_search_m<4, ch16<GRID>()>(cnt, off, sc, p.neigh, p.neigh_len, ws, EvalIq8{grid}, g);
+    coop_search_m<4, ch16<GRID>(), GRID == 1024>(cnt, off, sc, p.neigh, p.neigh_len, ws, EvalIq8{grid}, g);
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
         gi[m] = mk[m];
