@@ -198,7 +198,38 @@ def test_plan_and_check_mode(tmp_path, capsys):
     rp.write_text("attn_q q4_k\n")
     assert requant.main([p, str(tmp_path / "out"), str(rp), "--check"]) == 0
     assert "Q8_0" in capsys.readouterr().out and not os.path.exists(tmp_path / "out")
-    assert requant.main([p, str(tmp_path / "out"), str(rp), "--hessian=x"]) == 2
+    assert requant.main([p, str(tmp_path / "out"), str(rp), "--dump=x"]) == 2
+
+
+def test_hessian_files_and_plan(tmp_path):
+    """which tensors take error feedback: an expert tensor with a Hessian of its shape, an imatrix, a type rounded per
+    256-weight super-block and a float source; anything else is rounded plain, with the reason"""
+    hd = tmp_path / "h"
+    hd.mkdir()
+    assert requant.hess_file(str(hd), "blk.0.ffn_down_exps.weight") is None
+    np.save(hd / "blk.0.mid.npy", np.zeros((4, 512, 512)))
+    np.save(hd / "blk.0.counts.npy", np.full(4, 100.0))
+    np.save(hd / "blk.0.in_g.npy", np.zeros((4, 256, 256)))
+    assert requant.hess_file(str(hd), "blk.0.ffn_down_exps.weight") == (str(hd / "blk.0.mid.npy"),
+                                                                       str(hd / "blk.0.counts.npy"))
+    assert requant.hess_file(str(hd), "blk.0.ffn_up_exps.weight") is None
+    assert requant.hess_file(str(hd), "blk.0.ffn_up_exps.weight", gated=True)[0].endswith("blk.0.in_g.npy")
+    assert requant.hess_file(str(hd), "blk.0.attn_q.weight") is None
+    p = str(tmp_path / "m.gguf")
+    _sample_file(p)
+    r = gguf_io.GGUFReader(p)
+    im = {"blk.0.ffn_down_exps.weight": np.ones((4, 512), np.float32)}
+    hess = {"dir": str(hd)}
+    for typ, imat, note in ((T["IQ2_S"], im, None), (T["IQ2_S"], {}, "no imatrix data"),
+                            (T["Q8_0"], im, "not rounded per 256-weight super-block")):
+        s = requant.plan_shard(r, [(requant.re.compile("down"), typ)], imat, None, hess)[0]
+        if note is None:
+            assert s.hessian is not None and s.new_type == typ
+        else:
+            assert s.hessian is None and note in s.note
+    np.save(hd / "blk.0.mid.npy", np.zeros((3, 512, 512)))
+    s = requant.plan_shard(r, [(requant.re.compile("down"), T["IQ2_S"])], im, None, hess)[0]
+    assert s.hessian is None and "does not fit" in s.note and s.new_type == T["IQ2_S"]
 
 
 def test_shard_paths():
@@ -206,12 +237,20 @@ def test_shard_paths():
     assert requant.shard_paths("/m/x.gguf") == ["/m/x.gguf"]
 
 
+@pytest.fixture(scope="module")
+def gq():
+    """the library on device 0, loaded after torch has touched the GPU (torch wheels bundle a HIP runtime of the
+    same soname: initialised first, it serves both, and the later test modules' torch calls keep working)"""
+    import torch
+    torch.cuda.init()
+    return gpuq.load_gpuq(0)
+
+
 @pytest.mark.gpu
-def test_requant_gguf_matches_oracle(tmp_path):
+def test_requant_gguf_matches_oracle(tmp_path, gq):
     """a two-shard model: BF16 experts -> IQ2_XXS, MXFP4 experts -> IQ1_M, F32 -> Q8_0 and F16 -> Q4_K without an
     imatrix, 640-long rows -> IQ4_NL (the fallback), the rest copied; the second shard also with --only-matched"""
     from oracle import Oracle
-    gq = gpuq.load_gpuq(0)
     orc = Oracle(tables=gpuq.tables_path())
     rng = np.random.default_rng(11)
     ne0, ne1, nexp = 512, 32, 3
@@ -288,3 +327,63 @@ def test_requant_gguf_matches_oracle(tmp_path):
     full = gguf_io.GGUFReader(str(out / "m-00002-of-00002.gguf"))
     for t in r.tensors:
         assert np.array_equal(t.data, full.tensor(t.name).data)
+
+
+@pytest.mark.gpu
+def test_requant_hessian_matches_oracle_ldlq(tmp_path, oracle_lib, gq):
+    """--hessian: BF16 experts -> IQ2_S with error feedback, one Hessian per expert from blk.0.in.npy; expert 1's
+    row count is below LDLQ_MIN_ROWS (plain rounding). Each expert equals the oracle's LDLQ loop on the factor the
+    device builds from that expert's Hessian (or the oracle's plain quantization for expert 1)."""
+    import torch
+    from gpuq import ldlq
+    from test_ldlq_gpu import design, prepare_dev
+    ne0, ne1, nexp, typ = 512, 16, 3, T["IQ2_S"]
+    Hs, ims, ws = [], [], []
+    for e in range(nexp):
+        H, n, imatrix, W = design(ne1=ne1, ne0=ne0, seed=20 + e)
+        Hs.append(H)
+        ims.append(imatrix * (1 + e))
+        ws.append(W[0])
+    counts = np.array([n, 10, n], dtype=np.float64)
+    bits = np.stack(ws).view(np.uint32)
+    bf16 = ((bits + 0x7FFF + ((bits >> 16) & 1)) >> 16).astype(np.uint16)
+    wbf = (bf16.astype(np.uint32) << 16).view(np.float32)                     # the weights the file holds
+    hd = tmp_path / "hess"
+    hd.mkdir()
+    np.save(hd / "blk.0.in.npy", np.stack(Hs))
+    np.save(hd / "blk.0.counts.npy", counts)
+    src = str(tmp_path / "m.gguf")
+    with gguf_io.GGUFWriter(src) as w:
+        w.add_tensor_info("blk.0.ffn_up_exps.weight", (ne0, ne1, nexp), T["BF16"])
+        w.add_tensor_info("blk.0.ffn_down_exps.weight", (ne0, ne1, nexp), T["BF16"])   # no Hessian: plain
+        w.write_header()
+        w.write_tensor_data(bf16)
+        w.write_tensor_data(bf16)
+    imp = str(tmp_path / "im.gguf")
+    im_all = np.stack(ims).astype(np.float32)
+    with gguf_io.GGUFWriter(imp) as w:
+        for nm in ("blk.0.ffn_up_exps.weight", "blk.0.ffn_down_exps.weight"):
+            w.add_tensor_info(nm + ".in_sum2", (im_all.size,), T["F32"])
+            w.add_tensor_info(nm + ".counts", (nexp,), T["F32"])
+        w.write_header()
+        for _ in range(2):
+            w.write_tensor_data(im_all)
+            w.write_tensor_data(np.ones(nexp, np.float32))
+    rules = tmp_path / "rules.txt"
+    rules.write_text("ffn_(up|down)_exps iq2_s\n")
+    out = tmp_path / "out"
+    requant.run(src, str(out), str(rules), imp, gq=gq, hess={"dir": str(hd), "damp": 0.01, "order": "seq"})
+    r = gguf_io.GGUFReader(str(out / "m.gguf"))
+    rb = ne0 // 256 * 82
+    for e in range(nexp):
+        if counts[e] < requant.MIN_ROWS:
+            want = oracle_lib.quantize(typ, wbf[e], im_all[e])
+        else:
+            U, perm, _, _ = prepare_dev(torch, gq, Hs[e], counts[e], "seq")
+            want = oracle_lib.ldlq(typ, wbf[e][None][:, :, perm], U, im_all[e][perm][None], ldlq.slot_order(perm))[0][0]
+        got = r.tensor("blk.0.ffn_up_exps.weight").data.reshape(nexp, ne1 * rb)[e]
+        assert np.array_equal(got, want.reshape(-1)), "expert %d: %d bytes differ" % (e, int((got != want.reshape(-1)).sum()))
+        plain = oracle_lib.quantize(typ, wbf[e], im_all[e])
+        assert np.array_equal(r.tensor("blk.0.ffn_down_exps.weight").data.reshape(nexp, -1)[e], plain.reshape(-1))
+    # the feedback changed the experts it ran on
+    assert not np.array_equal(r.tensor("blk.0.ffn_up_exps.weight").data, r.tensor("blk.0.ffn_down_exps.weight").data)

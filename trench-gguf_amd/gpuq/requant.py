@@ -1,7 +1,7 @@
 """Re-quantize the tensors of a (split) GGUF that a rules file names, on the MI355X, and copy the rest byte for byte.
 
     python requant.py <in shard 1> <out dir> <rules file> [--imatrix=<imatrix.gguf>] [--check] [--gpu=N]
-                      [--only-matched]
+                      [--only-matched] [--hessian=<dir> [--damp=0.01] [--damp-iq1=D] [--order=seq|act] [--gated]]
 
 This is the plan-and-write part of the reference's tools/requant_experts.py (rules: 171-177; fallback types:
 180-192; imatrix normalization: 280-293; the per-shard plan: 420-470; the writer: 471-500) with its quantizer
@@ -10,10 +10,17 @@ BF16, Q8_0, MXFP4) on the GPU and quantizes every expert with its own imatrix ro
 by gguf_io (no gguf-py). The rules file holds one "<tensor name regex> <type>" a line (# comments); the first rule
 whose regex matches anywhere in the name wins.
 
-Not here (the reference's other paths): error-feedback rounding (--hessian / --dump; the library's gpuq_ldlq and
-gpuq_ldlq_dev serve it), the CPU quantizer, sources in other stored types and the fallback types that libgpuq does
-not produce (Q4_0, Q5_0, Q5_1, F16). A tensor that needs one of these stops the run with its name and the reason;
-nothing falls back to the CPU.
+--hessian=<dir> turns on error-feedback (LDLQ) rounding for the expert tensors the folder has a Hessian for, as the
+reference's driver does (tools/requant_experts.py:200-212, 520-600): blk.L.in.npy [n_expert, ne0, ne0] for
+ffn_gate/up_exps, blk.L.mid.npy for ffn_down_exps (blk.L.in_g / mid_g with --gated), blk.L.counts.npy the rows
+each expert's Hessian summed. Each expert runs libgpuq's whole LDLQ path (gpuq_ldlq: the factor and the loop on the
+device, the imatrix row as the importance); an expert with fewer than LDLQ_MIN_ROWS (64) rows is rounded plain.
+Sources for it: F32, F16 and BF16 (widened to f32 exactly on the host).
+
+Not here (the reference's other paths): --dump / --dense-dump Hessians, --weights other than imatrix, --sub, the
+CPU quantizer, sources in other stored types and the fallback types that libgpuq does not produce (Q4_0, Q5_0,
+Q5_1, F16). A tensor that needs one of these stops the run with its name and the reason; nothing falls back to the
+CPU.
 """
 import os
 import re
@@ -36,6 +43,10 @@ FALLBACK = {T["IQ1_S"]: T["IQ4_NL"], T["IQ1_M"]: T["IQ4_NL"], T["IQ2_XXS"]: T["I
 # the types ggml refuses to quantize without importance data
 NEEDS_IMATRIX = {T["IQ1_S"], T["IQ1_M"], T["IQ2_XXS"], T["IQ2_XS"], T["IQ2_S"]}
 SOURCES = (gpuq.F32, gpuq.F16, gpuq.BF16, gpuq.Q8_0, gpuq.MXFP4)   # stored types the library decodes
+# types whose quantizer is closed per 256-weight super-block: the LDLQ loop can feed back between super-blocks
+LDLQ_TYPES = {T["IQ1_S"], T["IQ1_M"], T["IQ2_XXS"], T["IQ2_XS"], T["IQ2_S"], T["IQ3_XXS"], T["IQ3_S"], T["IQ4_XS"],
+              T["Q4_K"], T["Q5_K"], T["Q6_K"]}
+MIN_ROWS = int(os.environ.get("LDLQ_MIN_ROWS", 64))   # an expert with fewer calibration rows is rounded plain
 
 
 class RequantError(RuntimeError):
@@ -98,19 +109,31 @@ def shard_paths(shard1):
     return [os.path.join(d, "%s-%05d-of-%s.gguf" % (m.group(1), i, m.group(3))) for i in range(1, int(m.group(3)) + 1)]
 
 
+def hess_file(hess_dir, name, gated=False):
+    """(Hessian .npy, counts .npy) of an expert tensor, or None when the folder has none for it"""
+    m = re.match(r"blk\.(\d+)\.ffn_(gate|up|down)_exps\.weight$", name)
+    if m is None:
+        return None
+    h = os.path.join(hess_dir, "blk.%s.%s%s.npy" % (m.group(1), "mid" if m.group(2) == "down" else "in",
+                                                   "_g" if gated else ""))
+    c = os.path.join(hess_dir, "blk.%s.counts.npy" % m.group(1))
+    return (h, c) if os.path.exists(h) and os.path.exists(c) else None
+
+
 class Step:
     """one tensor of the plan: kept (new_type None) or re-quantized to new_type, with or without its imatrix rows"""
-    __slots__ = ("tensor", "new_type", "nbytes", "imatrix", "note")
+    __slots__ = ("tensor", "new_type", "nbytes", "imatrix", "note", "hessian")
 
-    def __init__(self, tensor, new_type=None, nbytes=0, imatrix=None, note=""):
+    def __init__(self, tensor, new_type=None, nbytes=0, imatrix=None, note="", hessian=None):
         self.tensor, self.new_type, self.nbytes, self.imatrix, self.note = tensor, new_type, nbytes, imatrix, note
+        self.hessian = hessian          # (Hessian .npy, counts .npy) for error-feedback rounding, or None
 
 
-def plan_shard(reader, rules, imat, can_quantize=None):
+def plan_shard(reader, rules, imat, can_quantize=None, hess=None):
     """the plan of one shard (tools/requant_experts.py:420-470): the rule's type, fitted to the row length; an
     i-quant that needs an imatrix the file does not hold, or one of the wrong shape, leaves the tensor as it is; a
     type that takes one quantizes without it then. can_quantize(type, with_imatrix) -> bool is libgpuq's
-    gpuq_can_quantize (None: plan only)."""
+    gpuq_can_quantize (None: plan only). hess: {"dir", "gated"} for error-feedback rounding, or None."""
     plan = []
     for t in reader.tensors:
         typ = rule_type(rules, t.name)
@@ -146,11 +169,26 @@ def plan_shard(reader, rules, imat, can_quantize=None):
         if t.tensor_type not in SOURCES:
             raise RequantError("%s: stored as %s, which libgpuq does not decode (F32, F16, BF16, Q8_0, MXFP4)" % (
                 t.name, gguf_io.type_name(t.tensor_type)))
-        plan.append(Step(t, typ, gguf_io.tensor_bytes(typ, t.shape), im, note))
+        hf = None
+        if hess is not None and len(t.shape) == 3:
+            hf = hess_file(hess["dir"], t.name, hess.get("gated", False))
+            if hf is not None:
+                shp = np.load(hf[0], mmap_mode="r").shape
+                why = ("Hessian %s does not fit [%d x %d x %d]" % (shp, t.shape[2], t.shape[0], t.shape[0])
+                       if shp != (t.shape[2], t.shape[0], t.shape[0]) else
+                       "no imatrix" if im is None else
+                       "%s is not rounded per 256-weight super-block" % gguf_io.type_name(typ)
+                       if typ not in LDLQ_TYPES or t.shape[0] % 256 else
+                       "stored as %s (error feedback reads F32 / F16 / BF16)" % gguf_io.type_name(t.tensor_type)
+                       if t.tensor_type not in (gpuq.F32, gpuq.F16, gpuq.BF16) else None)
+                if why is not None:
+                    note = (note + "; " if note else "") + why + ": plain rounding"
+                    hf = None
+        plan.append(Step(t, typ, gguf_io.tensor_bytes(typ, t.shape), im, note, hf))
     return plan
 
 
-def quantize_tensor(gq, step, batch_floats):
+def quantize_tensor(gq, step, batch_floats, hess=None):
     """the re-quantized bytes of one tensor: gpuq_requantize_batch over groups of whole experts (source bytes as
     stored, each expert with its own imatrix row)"""
     t = step.tensor
@@ -161,6 +199,8 @@ def quantize_tensor(gq, step, batch_floats):
     dst_mat = step.nbytes // ne2
     per = max(1, min(ne2, batch_floats // (ne0 * ne1)))
     src = np.ascontiguousarray(t.data)        # (a view of the mapped file: read as the library copies it in)
+    if step.hessian is not None:
+        return quantize_tensor_ldlq(gq, step, hess or {}, out)
     for e0 in range(0, ne2, per):
         n = min(per, ne2 - e0)
         im = None
@@ -175,7 +215,37 @@ def quantize_tensor(gq, step, batch_floats):
     return out
 
 
-def write_shard(path, reader, plan, gq, batch_floats, only_matched=False, kv_src=None, log=print):
+def quantize_tensor_ldlq(gq, step, hess, out):
+    """error-feedback rounding, expert by expert: the expert's Hessian and row count from the folder, the whole LDLQ
+    path on the device (gpuq_ldlq), the expert's imatrix row as the importance; plain rounding for an expert with
+    fewer than MIN_ROWS rows"""
+    from gpuq import ldlq
+    t = step.tensor
+    ne0, ne1, ne2 = t.shape
+    typ = step.new_type
+    damp = hess.get("damp", 0.01)
+    if hess.get("damp_iq1") is not None and typ in (T["IQ1_S"], T["IQ1_M"]):
+        damp = hess["damp_iq1"]
+    H_all = np.load(step.hessian[0], mmap_mode="r")
+    counts = np.asarray(np.load(step.hessian[1])).reshape(-1)
+    W_all = t.f32()                                   # [ne2, ne1, ne0], exact for F32 / F16 / BF16
+    dst = out.reshape(ne2, -1)
+    for e in range(ne2):
+        n = float(counts[e])
+        w = np.ascontiguousarray(W_all[e], dtype=np.float32)
+        im = np.ascontiguousarray(step.imatrix[e], dtype=np.float32)
+        if n < MIN_ROWS:
+            got = gq.gpuq_quantize(typ, w.ctypes.data, dst[e].ctypes.data, ne1, ne0, im.ctypes.data)
+            if got != dst.shape[1]:
+                raise RequantError("%s: gpuq_quantize failed for expert %d" % (t.name, e))
+            continue
+        H = np.asarray(H_all[e], dtype=np.float64)
+        dst[e] = ldlq.quantize_matrix_host(gq, typ, w, H, n, im, damp=damp,
+                                           order=hess.get("order", "seq")).reshape(-1)
+    return out
+
+
+def write_shard(path, reader, plan, gq, batch_floats, only_matched=False, kv_src=None, log=print, hess=None):
     """the output GGUF: the source's key/values as stored (kv_src's for only_matched, split keys dropped), then
     every tensor of the plan in the source's order, re-quantized or copied"""
     steps = [s for s in plan if s.new_type is not None] if only_matched else plan
@@ -193,13 +263,14 @@ def write_shard(path, reader, plan, gq, batch_floats, only_matched=False, kv_src
                 w.write_tensor_data(s.tensor.data)
             else:
                 t0 = time.time()
-                w.write_tensor_data(quantize_tensor(gq, s, batch_floats))
-                log("  %-34s %s -> %s  %.2f s" % (s.tensor.name, gguf_io.type_name(s.tensor.tensor_type),
-                                                  gguf_io.type_name(s.new_type), time.time() - t0))
+                w.write_tensor_data(quantize_tensor(gq, s, batch_floats, hess))
+                log("  %-34s %s -> %s%s  %.2f s" % (s.tensor.name, gguf_io.type_name(s.tensor.tensor_type),
+                                                    gguf_io.type_name(s.new_type),
+                                                    " (error feedback)" if s.hessian else "", time.time() - t0))
 
 
 def run(shard1, out_dir, rules_path, imatrix_path=None, check=False, device=0, only_matched=False, gq=None,
-        log=print):
+        log=print, hess=None):
     """re-quantize every shard; returns (source bytes, output bytes) of the re-quantized tensors"""
     rules = read_rules(rules_path)
     imat = read_imatrix(imatrix_path) if imatrix_path else {}
@@ -219,7 +290,7 @@ def run(shard1, out_dir, rules_path, imatrix_path=None, check=False, device=0, o
         r = first if sh == paths[0] else gguf_io.GGUFReader(sh)
         out = os.path.join(out_dir, os.path.basename(sh))
         log("%s -> %s" % (sh, out))
-        plan = plan_shard(r, rules, imat, can)
+        plan = plan_shard(r, rules, imat, can, hess)
         for s in plan:
             if s.note:
                 log("  %s: %s" % (s.tensor.name, s.note))
@@ -234,7 +305,7 @@ def run(shard1, out_dir, rules_path, imatrix_path=None, check=False, device=0, o
         if only_matched and not any(s.new_type is not None for s in plan):
             log("  nothing re-quantized in this shard: no file (--only-matched)")
             continue
-        write_shard(out, r, plan, gq, batch_floats, only_matched, first if only_matched else None, log)
+        write_shard(out, r, plan, gq, batch_floats, only_matched, first if only_matched else None, log, hess)
     log("re-quantized tensors: %.3f GiB -> %.3f GiB" % (old / 2**30, new / 2**30))
     return old, new
 
@@ -243,7 +314,8 @@ def main(argv=None):
     argv = sys.argv[1:] if argv is None else argv
     flags = [a for a in argv if a.startswith("--")]
     args = [a for a in argv if not a.startswith("--")]
-    known = ("--imatrix=", "--gpu=", "--check", "--only-matched")
+    known = ("--imatrix=", "--gpu=", "--check", "--only-matched", "--hessian=", "--damp=", "--damp-iq1=",
+             "--order=", "--gated")
     bad = [f for f in flags if not f.startswith(known)]
     if len(args) != 3 or bad:
         print(__doc__.split("\n\n")[1], file=sys.stderr)
@@ -252,8 +324,17 @@ def main(argv=None):
         return 2
     imat = next((f.split("=", 1)[1] for f in flags if f.startswith("--imatrix=")), None)
     dev = int(next((f.split("=", 1)[1] for f in flags if f.startswith("--gpu=")), "0"))
+    opt = {f.split("=", 1)[0]: f.split("=", 1)[1] for f in flags if "=" in f}
+    hess = None
+    if "--hessian" in opt:
+        hess = {"dir": opt["--hessian"], "damp": float(opt.get("--damp", 0.01)), "gated": "--gated" in flags,
+                "damp_iq1": float(opt["--damp-iq1"]) if "--damp-iq1" in opt else None,
+                "order": opt.get("--order", "seq")}
+        if hess["order"] not in ("seq", "act"):
+            print("--order is seq or act", file=sys.stderr)
+            return 2
     try:
-        run(args[0], args[1], args[2], imat, "--check" in flags, dev, "--only-matched" in flags)
+        run(args[0], args[1], args[2], imat, "--check" in flags, dev, "--only-matched" in flags, hess=hess)
     except RequantError as e:
         print("error: %s" % e, file=sys.stderr)
         return 1
