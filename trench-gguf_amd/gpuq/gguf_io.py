@@ -122,14 +122,18 @@ class TensorInfo:
 
     def f32(self):
         """the tensor as float32 (stored F32 / F16 / BF16 only; numpy order: ne0 last)"""
-        shp = tuple(reversed(self.shape))
-        if self.tensor_type == 0:
-            return self.data.view(np.float32).reshape(shp)
-        if self.tensor_type == 1:
-            return self.data.view(np.float16).astype(np.float32).reshape(shp)
-        if self.tensor_type == 30:
-            return (self.data.view(np.uint16).astype(np.uint32) << 16).view(np.float32).reshape(shp)
-        raise ValueError("%s is stored as %s, not a float type" % (self.name, type_name(self.tensor_type)))
+        return widen(self.tensor_type, self.data, self.name).reshape(tuple(reversed(self.shape)))
+
+
+def widen(ttype, raw, name="tensor"):
+    """stored F32 / F16 / BF16 bytes as float32, exactly (a flat array)"""
+    if ttype == 0:
+        return raw.view(np.float32)
+    if ttype == 1:
+        return raw.view(np.float16).astype(np.float32)
+    if ttype == 30:
+        return (raw.view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+    raise ValueError("%s is stored as %s, not a float type" % (name, type_name(ttype)))
 
 
 class _Cursor:

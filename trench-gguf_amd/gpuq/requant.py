@@ -198,9 +198,9 @@ def quantize_tensor(gq, step, batch_floats, hess=None):
     src_mat = t.n_bytes // ne2
     dst_mat = step.nbytes // ne2
     per = max(1, min(ne2, batch_floats // (ne0 * ne1)))
-    src = np.ascontiguousarray(t.data)        # (a view of the mapped file: read as the library copies it in)
     if step.hessian is not None:
         return quantize_tensor_ldlq(gq, step, hess or {}, out)
+    src = np.ascontiguousarray(t.data)        # (a view of the mapped file: read as the library copies it in)
     for e0 in range(0, ne2, per):
         n = min(per, ne2 - e0)
         im = None
@@ -228,11 +228,11 @@ def quantize_tensor_ldlq(gq, step, hess, out):
         damp = hess["damp_iq1"]
     H_all = np.load(step.hessian[0], mmap_mode="r")
     counts = np.asarray(np.load(step.hessian[1])).reshape(-1)
-    W_all = t.f32()                                   # [ne2, ne1, ne0], exact for F32 / F16 / BF16
+    per = t.n_bytes // ne2
     dst = out.reshape(ne2, -1)
     for e in range(ne2):
         n = float(counts[e])
-        w = np.ascontiguousarray(W_all[e], dtype=np.float32)
+        w = np.ascontiguousarray(gguf_io.widen(t.tensor_type, t.data[e * per:(e + 1) * per], t.name).reshape(ne1, ne0))
         im = np.ascontiguousarray(step.imatrix[e], dtype=np.float32)
         if n < MIN_ROWS:
             got = gq.gpuq_quantize(typ, w.ctypes.data, dst[e].ctypes.data, ne1, ne0, im.ctypes.data)
