@@ -504,6 +504,7 @@ struct KQ2K {
 // block: hmask[32] qs[64] scales[12] d (110 bytes)
 struct KQ3K {
     static constexpr int BS = QK, G = 16, N = 16, BB = 110, TAB = 0;
+    static constexpr int WPE = 3;    // 168 VGPRs, no spill: three waves a SIMD (11% faster than two)
     static DEV void stage(const QParams &, uint8_t *) {}
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *,
                           const QParams &) {
@@ -874,6 +875,7 @@ DEV float iq4_block(const float (&xb)[32], const float (&weight)[32], Lv<32> &Lb
 // IQ4_XS: block d scales_h scales_l[4] qs[128] (136 bytes); lane g = sub-block g
 struct KIQ4XS {
     static constexpr int BS = QK, G = 8, N = 32, BB = 136, TAB = 64;
+    static constexpr int WPE = 3;    // three waves a SIMD: 7% faster than two, for 140 bytes a lane of spill
     static DEV void stage(const QParams &, uint8_t *lds) {
         if (threadIdx.x < 16) ((float *)lds)[threadIdx.x] = k_iq4f[threadIdx.x];
     }
