@@ -378,6 +378,7 @@ def main():
     torch.cuda.init()
     import gpuq
     from oracle import Oracle
+    os.environ["GPUQ_ALLOW_SYNTHETIC_TABLES"] = "1"      # the repository's stand-in IQ tables (a benchmark run)
     gq = gpuq.load_gpuq(0)
     orc = Oracle(tables=gpuq.tables_path())
     orc_ops = Oracle("liboracle_ops.so", tables=gpuq.tables_path())

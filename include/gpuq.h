@@ -27,7 +27,10 @@ extern "C" {
 /* gpuq/gpuq.hip:2059 gpuq_init. Selects the device and loads the search / dequantizer tables. 0 ok; 1 no such
  * device; 2 cannot open the file; 3 short or malformed record; 4 device allocation failed; 6 a table fails the
  * consistency checks (a point whose key does not map back to it, or a reachable key with no candidate). A file with
- * no records returns 0 (the k-quants, Q8_0 and IQ4 need no tables). */
+ * no records returns 0 (the k-quants, Q8_0 and IQ4 need no tables). A file that carries the stand-in mark (a record
+ * of type 0x53594e54, written by this package's table generator, never by ggml's) loads its IQ1/IQ2/IQ3 tables only
+ * when the environment sets GPUQ_ALLOW_SYNTHETIC_TABLES=1; otherwise it returns 0 with those types unavailable
+ * (gpuq_can_quantize / gpuq_can_dequantize_type report 0), since their grid indices would not be ggml's. */
 int gpuq_init(const char *tables_path, int device);
 
 /* gpuq/gpuq.hip:2082 gpuq_block_bytes: bytes of one block of the type, 0 for an unknown type */
@@ -60,7 +63,8 @@ size_t gpuq_requantize_batch(int src_type, const void *raw, int type, void *dst,
 size_t gpuq_quantize_dev(int type, const float *d_x, void *d_dst, int64_t nblocks, const float *d_qw, int64_t qw_mod,
                          int64_t qw_div, void *stream);
 
-/* gpuq/gpuq.hip:2292 gpuq_can_dequantize_type: 1 for the i-quants with a dequantizer grid, and IQ4_XS */
+/* gpuq/gpuq.hip:2292 gpuq_can_dequantize_type: 1 for the i-quants with a dequantizer grid and IQ4_XS (the
+ * reference's set), and the k-quants Q2_K..Q6_K (an addition: the reference reads them back through ggml) */
 int gpuq_can_dequantize_type(int type);
 
 /* gpuq/gpuq.hip:2302 gpuq_dequantize_dev: nblocks blocks (device) -> nblocks*256 f32 (device), ggml's to_float */
@@ -71,9 +75,10 @@ size_t gpuq_dequantize_src_dev(int src_type, const void *d_raw, float *d_out, in
 
 /* ---- additions (no counterpart in the reference) ---- */
 
-/* Device-resident requantize: nmat matrices of nrow x n_per_row values stored as src_type (F32, BF16 or MXFP4,
- * decoded in registers inside the quantize kernel) -> d_dst, matrix m weighted by d_imatrix + m*n_per_row (or
- * none). For callers that keep the source in HBM (the streaming driver, the benchmark). */
+/* Device-resident requantize: nmat matrices of nrow x n_per_row values stored as src_type (F32, F16, BF16, Q8_0 or
+ * MXFP4, decoded in registers inside the quantize kernel) -> d_dst, matrix m weighted by d_imatrix + m*n_per_row (or
+ * none). d_raw 16-byte aligned for F32 / F16 / BF16 (2-byte for Q8_0), n_per_row a multiple of 32. For callers that
+ * keep the source in HBM (the streaming driver, the benchmark). */
 size_t gpuq_requantize_dev(int src_type, const void *d_raw, int type, void *d_dst, int64_t nmat, int64_t nrow,
                            int64_t n_per_row, const float *d_imatrix, void *stream);
 
@@ -83,8 +88,10 @@ size_t gpuq_requantize_dev(int src_type, const void *d_raw, int type, void *d_ds
  * permuted column order (updated in place), d_u [ne0][ne0] f64 row-major upper factor of the permuted inverse
  * Hessian, d_qw [nmat][ne0] f32 importances in permuted order, blk_order (host) the output slot of each permuted
  * 256-column block, d_out [nmat][ne1][ne0/256 blocks]. The f64 solve and update use fixed-order FMA chains (the CPU
- * oracle computes the same ones). Types: the i-quants with a dequantizer grid and IQ4_XS. Asynchronous on `stream`
- * (part of each update runs on an internal stream that is joined back into `stream` before the call returns). */
+ * oracle computes the same ones). Types: the i-quants with a dequantizer grid, IQ4_XS and Q2_K..Q6_K. Asynchronous
+ * on `stream` (part of each update runs on an internal stream that is joined back into `stream` before the call
+ * returns). Calls share one library scratch buffer; each call's launches wait for the previous call's, on whatever
+ * stream that one ran, so calls from several streams are ordered on the device. */
 size_t gpuq_ldlq_dev(int type, float *d_wp, const double *d_u, int64_t u_stride, const float *d_qw, int64_t nmat,
                      int64_t ne1, int64_t ne0, const int64_t *blk_order, int feedback, void *d_out, void *stream);
 
@@ -105,14 +112,21 @@ int gpuq_hessian_accumulate_dev(const float *d_X, int64_t nrows, int64_t ne0, do
 int gpuq_prepare_hessian_dev(const double *d_H, int64_t ne0, double n, double damp, int order, double *d_U,
                              int64_t *perm, double *diag_n, unsigned char *dead, void *stream);
 
+/* The 'schur' importance of each 256-column block of an LDLQ factor, replacing the numpy / torch inverse of
+ * tools/ldlq.py:90-93, 424-426 (diag((U_BB^T U_BB)^-1)): d_u [ne0][ne0] f64 upper factor (device) -> d_w [nrep][ne0]
+ * f32 (device; the same values in each of the nrep rows, one a matrix that shares U), in a fixed summation order the
+ * CPU oracle repeats. Asynchronous on `stream`. Returns 0; 1 bad arguments; 4 a HIP error. */
+int gpuq_schur_weights_dev(const double *d_u, int64_t ne0, float *d_w, int64_t nrep, void *stream);
+
 /* The LDLQ loop from host memory, with no framework on the caller's side: the reference's tools/ldlq.py:71-107
- * (quantize_matrix with weights = "imatrix") with the factor of gpuq_prepare_hessian_dev. W [nmat][ne1][ne0] f32
- * (original column order, not modified), H [ne0][ne0] f64 shared by all matrices (h_stride 0) or one a matrix
- * (h_stride ne0*ne0), n and damp and order as gpuq_prepare_hessian_dev, imatrix [nmat][ne0] (NULL only for a type that
- * takes none). Writes every matrix's GGUF bytes to dst (blocks in their original slots) and returns their count, or 0
- * on an error. Serializes on an internal lock; synchronous. */
+ * (quantize_matrix) with the factor of gpuq_prepare_hessian_dev. W [nmat][ne1][ne0] f32 (original column order, not
+ * modified), H [ne0][ne0] f64 shared by all matrices (h_stride 0) or one a matrix (h_stride ne0*ne0), n and damp and
+ * order as gpuq_prepare_hessian_dev. weights (the reference's `weights`): 0 'imatrix' (imatrix [nmat][ne0]; NULL only
+ * for a type that takes none), 1 'diag' (diag(H)/n), 2 'schur' (gpuq_schur_weights_dev); imatrix NULL for 1 and 2.
+ * Writes every matrix's GGUF bytes to dst (blocks in their original slots) and returns their count, or 0 on an error.
+ * Serializes on an internal lock; synchronous. */
 size_t gpuq_ldlq(int type, const float *W, const double *H, int64_t h_stride, double n, double damp, int order,
-                 const float *imatrix, int64_t nmat, int64_t ne1, int64_t ne0, void *dst);
+                 int weights, const float *imatrix, int64_t nmat, int64_t ne1, int64_t ne0, void *dst);
 
 /* Reads and clears the flag the kernels set where the reference would trap (a key with no candidate point: non-
  * finite input or an inconsistent table). Synchronizes the device. */

@@ -2026,14 +2026,105 @@ static void d_iq4_xs(const uint8_t *x, float *y) {
     }
 }
 
+/* ggml's to_float of the k-quants (ggml-quants.c dequantize_row_q2_K .. q6_K, which the reference calls through
+ * libggml-base for its LDLQ loop, tools/requant_experts.py:588-591), in ggml's loop order over the block layouts the
+ * quantizers above write: y = d * sc * q - dmin * m, every product and difference rounded as written. */
+static void d_q2_k(const uint8_t *x, float *y) {
+    const float d = f16_to_f32(get16(x + 80)), dmin = f16_to_f32(get16(x + 82));
+    const uint8_t *q = x + 16;
+    int is = 0;
+    for (int n = 0; n < QK; n += 128) {
+        for (int shift = 0; shift < 8; shift += 2) {
+            for (int h = 0; h < 2; ++h) {
+                const uint8_t sc = x[is++];
+                const float dl = d * (sc & 0xF), ml = dmin * (sc >> 4);
+                for (int l = 0; l < 16; ++l) *y++ = dl * (int8_t)((q[l + 16 * h] >> shift) & 3) - ml;
+            }
+        }
+        q += 32;
+    }
+}
+static void d_q3_k(const uint8_t *x, float *y) {
+    const uint8_t *hm = x, *q = x + 32, *s = x + 96;
+    const float d = f16_to_f32(get16(x + 108));
+    int8_t sc[16];   /* the 16 6-bit scales: low 4 bits from nibbles of s[0..7], high 2 bits from s[8..11] */
+    for (int i = 0; i < 16; ++i) {
+        const int lo = i < 8 ? (s[i] & 0xF) : (s[i - 8] >> 4);
+        sc[i] = (int8_t)(lo | (((s[8 + i % 4] >> (2 * (i / 4))) & 3) << 4));
+    }
+    int is = 0;
+    uint8_t m = 1;
+    for (int n = 0; n < QK; n += 128) {
+        for (int shift = 0; shift < 8; shift += 2) {
+            for (int h = 0; h < 2; ++h) {
+                const float dl = d * (sc[is++] - 32);
+                for (int l = 0; l < 16; ++l)
+                    *y++ = dl * ((int8_t)((q[l + 16 * h] >> shift) & 3) - ((hm[l + 16 * h] & m) ? 0 : 4));
+            }
+            m <<= 1;
+        }
+        q += 32;
+    }
+}
+static void d_q45_k(const uint8_t *x, float *y, int five) {
+    const float d = f16_to_f32(get16(x)), dmin = f16_to_f32(get16(x + 2));
+    const uint8_t *s = x + 4, *qh = x + 16, *ql = x + (five ? 48 : 16);
+    uint8_t u1 = 1, u2 = 2;
+    for (int j = 0, is = 0; j < QK; j += 64, is += 2) {
+        uint8_t sc, m;
+        k4_unpack(is, s, &sc, &m);
+        const float d1 = d * sc, m1 = dmin * m;
+        k4_unpack(is + 1, s, &sc, &m);
+        const float d2 = d * sc, m2 = dmin * m;
+        for (int l = 0; l < 32; ++l) *y++ = d1 * ((ql[l] & 0xF) + (five && (qh[l] & u1) ? 16 : 0)) - m1;
+        for (int l = 0; l < 32; ++l) *y++ = d2 * ((ql[l] >> 4) + (five && (qh[l] & u2) ? 16 : 0)) - m2;
+        ql += 32;
+        u1 <<= 2;
+        u2 <<= 2;
+    }
+}
+static void d_q6_k(const uint8_t *x, float *y) {
+    const float d = f16_to_f32(get16(x + 208));
+    const uint8_t *ql = x, *qh = x + 128;
+    const int8_t *sc = (const int8_t *)(x + 192);
+    for (int n = 0; n < QK; n += 128) {
+        for (int l = 0; l < 32; ++l) {
+            const int is = l / 16;
+            const int8_t q1 = (int8_t)((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32;
+            const int8_t q2 = (int8_t)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+            const int8_t q3 = (int8_t)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+            const int8_t q4 = (int8_t)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+            y[l] = d * sc[is + 0] * q1;
+            y[l + 32] = d * sc[is + 2] * q2;
+            y[l + 64] = d * sc[is + 4] * q3;
+            y[l + 96] = d * sc[is + 6] * q4;
+        }
+        y += 128;
+        ql += 64;
+        qh += 32;
+        sc += 8;
+    }
+}
+
 size_t gqo_dequantize(int type, const void *src, float *dst, int64_t n) {
     const uint8_t *x = (const uint8_t *)src;
     const size_t bb = gqo_block_bytes(type);
     const int bs = gqo_block_len(type);
     if (!bb || n < 0 || n % bs) return 0;
     const int64_t nb = n / bs;
-    if (type == GQO_IQ4_XS) {
-        for (int64_t b = 0; b < nb; ++b) d_iq4_xs(x + b * bb, dst + b * QK);
+    if (type == GQO_IQ4_XS || (type >= GQO_Q2_K && type <= GQO_Q6_K)) {
+        for (int64_t b = 0; b < nb; ++b) {
+            const uint8_t *xb = x + b * bb;
+            float *y = dst + b * QK;
+            switch (type) {
+                case GQO_IQ4_XS: d_iq4_xs(xb, y); break;
+                case GQO_Q2_K: d_q2_k(xb, y); break;
+                case GQO_Q3_K: d_q3_k(xb, y); break;
+                case GQO_Q4_K: d_q45_k(xb, y, 0); break;
+                case GQO_Q5_K: d_q45_k(xb, y, 1); break;
+                default: d_q6_k(xb, y); break;
+            }
+        }
         return (size_t)n * 4;
     }
     if (type == GQO_Q8_0) return gqo_decode_src(GQO_Q8_0, src, dst, n);
@@ -2191,4 +2282,25 @@ size_t gqo_ldlq(int type, float *Wp, const double *U, const float *qw, int64_t n
     }
     free(raw); free(q); free(blk); free(Es);
     return ok ? (size_t)nmat * ne1 * nblk * bb : 0;
+}
+
+/* ------------------------------------------------------------------ the 'schur' importance, fixed order
+ * tools/ldlq.py:90-93: qw = diag((U_BB^T U_BB)^-1) for each 256-column diagonal block U_BB of the factor (there
+ * np.linalg.inv). (U_BB^T U_BB)^-1 = X X^T with X = U_BB^-1, so qw[i] is the squared norm of X's row i, which comes
+ * from X U_BB = I by substitution along the row: x_t = ((t == i) - sum_{s=i}^{t-1} x_s U[s][t]) / U[t][t], each sum an
+ * fma chain over s ascending from 0.0, and qw[i] = (float)(sum_t x_t^2), an fma chain over t ascending from 0.0. */
+void gqo_schur_weights(const double *U, int64_t ne0, float *w) {
+    double acc[QK];
+    for (int64_t c0 = 0; c0 + QK <= ne0; c0 += QK) {
+        for (int i = 0; i < QK; ++i) {
+            for (int j = 0; j < QK; ++j) acc[j] = 0.0;
+            double ws = 0.0;
+            for (int t = i; t < QK; ++t) {
+                const double x = ((t == i ? 1.0 : 0.0) - acc[t]) / U[(c0 + t) * ne0 + c0 + t];
+                ws = fma(x, x, ws);
+                for (int j = t + 1; j < QK; ++j) acc[j] = fma(x, U[(c0 + t) * ne0 + c0 + j], acc[j]);
+            }
+            w[c0 + i] = (float)ws;
+        }
+    }
 }

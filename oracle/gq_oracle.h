@@ -63,6 +63,10 @@ size_t gqo_requantize_batch_mt(int src_type, const void *raw, int type, void *ds
 size_t gqo_ldlq(int type, float *Wp, const double *U, const float *qw, int64_t nmat, int64_t ne1, int64_t ne0,
                 const int64_t *blk_order, int feedback, void *out);
 
+/* The 'schur' importance (tools/ldlq.py:90-93, diag((U_BB^T U_BB)^-1) of each 256-column block of U [ne0][ne0] f64
+ * row major, upper triangle read) in a fixed summation order, see gq_oracle.c: w [ne0] f32. */
+void gqo_schur_weights(const double *U, int64_t ne0, float *w);
+
 /* op counter (built with -DGQO_COUNT_OPS only; 0 otherwise) */
 uint64_t gqo_ops_read_reset(void);
 

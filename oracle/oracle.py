@@ -54,6 +54,7 @@ class Oracle:
                                               ctypes.c_int]
         L.gqo_ldlq.restype = _sz
         L.gqo_ldlq.argtypes = [ctypes.c_int, _vp, _vp, _vp, _i64, _i64, _i64, _vp, ctypes.c_int, _vp]
+        L.gqo_schur_weights.argtypes = [_vp, _i64, _vp]
         L.gqo_ops_read_reset.restype = ctypes.c_uint64
         if tables is not None:
             rc = L.gqo_load_tables(tables.encode())
@@ -117,6 +118,13 @@ class Oracle:
         if got != out.nbytes:
             raise RuntimeError("oracle ldlq failed")
         return out, Wp
+
+    def schur_weights(self, U):
+        """U [ne0, ne0] f64 -> [ne0] f32, diag((U_BB^T U_BB)^-1) of each 256-column block (fixed order)"""
+        U = np.ascontiguousarray(U, dtype=np.float64)
+        w = np.empty(U.shape[0], dtype=np.float32)
+        self.lib.gqo_schur_weights(U.ctypes.data, U.shape[0], w.ctypes.data)
+        return w
 
     def fp32_to_fp16(self, f):
         return self.lib.gqo_fp32_to_fp16(f)

@@ -12,6 +12,9 @@ for p in (os.path.join(ROOT, "oracle"), os.path.join(PKG, "gpuq"), PKG):
         sys.path.insert(0, p)
 
 TABLES = os.path.join(PKG, "gpuq", "gpuq_tables.bin")
+# the repository's table file holds stand-in IQ codebooks (ggml's are not available here): the library loads them
+# only when asked to, which the tests do
+os.environ["GPUQ_ALLOW_SYNTHETIC_TABLES"] = "1"
 REF_LIB = os.path.join(ROOT, "oracle", "_ref", "libgpuq_ref.so")
 
 

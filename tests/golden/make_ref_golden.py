@@ -19,7 +19,9 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, os.path.join(ROOT, "tests"))
+sys.path.insert(0, os.path.join(ROOT, "trench-gguf_amd", "gpuq"))
 from conftest import REF_LIB, TABLES, selftest_matrices  # noqa: E402
+import tables  # noqa: E402
 
 ROWS = [0, 1, 8, 9, 16, 17, 32, 33, 48, 49, 64, 65, 100, 101, 200, 201]
 COLS = 1024
@@ -51,7 +53,7 @@ def main():
     assert lib.gpuq_init(TABLES.encode(), 0) == 0
     xs, ims = golden_inputs()
     out = {"meta_inputs": np.array(sha(np.stack(xs)) + sha(np.stack(ims))),
-           "meta_tables": np.array(hashlib.sha256(open(TABLES, "rb").read()).hexdigest())}
+           "meta_tables": np.array(tables.content_sha(TABLES))}
     for t in TYPES:
         bs = 32 if t in (8, 20) else 256
         for with_im in ([False] if t == 8 else [True, False] if t in NO_IM else [True]):

@@ -58,4 +58,5 @@ def test_nothing_quantizes_before_init(lib):
     assert lib.gpuq_can_dequantize_type(16) == 0
     assert lib.gpuq_quantize_dev(16, None, None, 1, None, 1, 1, None) == 0
     assert lib.gpuq_prepare_hessian_dev(None, 256, 1.0, 0.01, 0, None, None, None, None, None) == 1
-    assert lib.gpuq_ldlq(22, None, None, 0, 1.0, 0.01, 0, None, 1, 1, 256, None) == 0
+    assert lib.gpuq_ldlq(22, None, None, 0, 1.0, 0.01, 0, 0, None, 1, 1, 256, None) == 0
+    assert lib.gpuq_schur_weights_dev(None, 256, None, 1, None) == 1

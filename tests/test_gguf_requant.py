@@ -221,12 +221,16 @@ def test_hessian_files_and_plan(tmp_path):
     im = {"blk.0.ffn_down_exps.weight": np.ones((4, 512), np.float32)}
     hess = {"dir": str(hd)}
     for typ, imat, note in ((T["IQ2_S"], im, None), (T["IQ2_S"], {}, "no imatrix data"),
-                            (T["Q8_0"], im, "not rounded per 256-weight super-block")):
+                            (T["Q8_0"], im, "not rounded per 256-weight super-block"), (T["Q4_K"], im, None),
+                            (T["Q6_K"], im, None), (T["Q3_K"], im, "not rounded per 256-weight super-block")):
         s = requant.plan_shard(r, [(requant.re.compile("down"), typ)], imat, None, hess)[0]
         if note is None:
             assert s.hessian is not None and s.new_type == typ
         else:
             assert s.hessian is None and note in s.note
+    # a library that cannot read a type back rounds it plain, with the reason (instead of failing mid-run)
+    s = requant.plan_shard(r, [(requant.re.compile("down"), T["Q4_K"])], im, None, hess, can_ldlq=lambda t: False)[0]
+    assert s.hessian is None and "cannot read Q4_K back" in s.note and s.new_type == T["Q4_K"]
     np.save(hd / "blk.0.mid.npy", np.zeros((3, 512, 512)))
     s = requant.plan_shard(r, [(requant.re.compile("down"), T["IQ2_S"])], im, None, hess)[0]
     assert s.hessian is None and "does not fit" in s.note and s.new_type == T["IQ2_S"]
@@ -330,14 +334,16 @@ def test_requant_gguf_matches_oracle(tmp_path, gq):
 
 
 @pytest.mark.gpu
-def test_requant_hessian_matches_oracle_ldlq(tmp_path, oracle_lib, gq):
-    """--hessian: BF16 experts -> IQ2_S with error feedback, one Hessian per expert from blk.0.in.npy; expert 1's
-    row count is below LDLQ_MIN_ROWS (plain rounding). Each expert equals the oracle's LDLQ loop on the factor the
-    device builds from that expert's Hessian (or the oracle's plain quantization for expert 1)."""
+@pytest.mark.parametrize("tname,weights", [("IQ2_S", "imatrix"), ("Q4_K", "imatrix"), ("IQ2_XXS", "schur")])
+def test_requant_hessian_matches_oracle_ldlq(tmp_path, oracle_lib, gq, tname, weights):
+    """--hessian: BF16 experts -> an i-quant or k-quant with error feedback, one Hessian per expert from blk.0.in.npy;
+    expert 1's row count is below LDLQ_MIN_ROWS (plain rounding). Each expert equals the oracle's LDLQ loop on the
+    factor the device builds from that expert's Hessian, with the --weights importance (or the oracle's plain
+    quantization for expert 1)."""
     import torch
     from gpuq import ldlq
     from test_ldlq_gpu import design, prepare_dev
-    ne0, ne1, nexp, typ = 512, 16, 3, T["IQ2_S"]
+    ne0, ne1, nexp, typ = 512, 16, 3, T[tname]
     Hs, ims, ws = [], [], []
     for e in range(nexp):
         H, n, imatrix, W = design(ne1=ne1, ne0=ne0, seed=20 + e)
@@ -370,17 +376,20 @@ def test_requant_hessian_matches_oracle_ldlq(tmp_path, oracle_lib, gq):
             w.write_tensor_data(im_all)
             w.write_tensor_data(np.ones(nexp, np.float32))
     rules = tmp_path / "rules.txt"
-    rules.write_text("ffn_(up|down)_exps iq2_s\n")
+    rules.write_text("ffn_(up|down)_exps %s\n" % tname.lower())
     out = tmp_path / "out"
-    requant.run(src, str(out), str(rules), imp, gq=gq, hess={"dir": str(hd), "damp": 0.01, "order": "seq"})
+    print("case requant --hessian %s weights=%s" % (tname, weights), flush=True)
+    requant.run(src, str(out), str(rules), imp, gq=gq,
+                hess={"dir": str(hd), "damp": 0.01, "order": "seq", "weights": weights})
     r = gguf_io.GGUFReader(str(out / "m.gguf"))
-    rb = ne0 // 256 * 82
+    rb = ne0 // 256 * gq.gpuq_block_bytes(typ)
     for e in range(nexp):
         if counts[e] < requant.MIN_ROWS:
             want = oracle_lib.quantize(typ, wbf[e], im_all[e])
         else:
             U, perm, _, _ = prepare_dev(torch, gq, Hs[e], counts[e], "seq")
-            want = oracle_lib.ldlq(typ, wbf[e][None][:, :, perm], U, im_all[e][perm][None], ldlq.slot_order(perm))[0][0]
+            qw = im_all[e][perm] if weights == "imatrix" else oracle_lib.schur_weights(U)
+            want = oracle_lib.ldlq(typ, wbf[e][None][:, :, perm], U, qw[None], ldlq.slot_order(perm))[0][0]
         got = r.tensor("blk.0.ffn_up_exps.weight").data.reshape(nexp, ne1 * rb)[e]
         assert np.array_equal(got, want.reshape(-1)), "expert %d: %d bytes differ" % (e, int((got != want.reshape(-1)).sum()))
         plain = oracle_lib.quantize(typ, wbf[e], im_all[e])

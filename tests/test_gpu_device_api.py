@@ -1,7 +1,8 @@
 """The device-pointer entry points this library adds or keeps, against the oracle on the same bytes:
-gpuq_requantize_dev (source bytes in HBM decoded inside the quantize kernel: F32, BF16 and MXFP4, several matrices of
-an odd row count, one imatrix row a matrix, every type) and gpuq_dequantize_src_dev (every source encoding,
-gpuq/gpuq.hip:2323-2328 of the reference), plus the argument checks that answer 0 before any launch."""
+gpuq_requantize_dev (source bytes in HBM decoded inside the quantize kernel: F32, F16, BF16, Q8_0 and MXFP4, several
+matrices of an odd row count, one imatrix row a matrix, every type), gpuq_dequantize_src_dev (every source encoding,
+gpuq/gpuq.hip:2323-2328 of the reference), gpuq_dequantize_dev of the k-quants, the argument checks that answer 0
+before any launch, and the stand-in table guard of gpuq_init."""
 import numpy as np
 import pytest
 
@@ -39,7 +40,7 @@ def source(oracle_lib, src, x, seed):
     return raw.reshape(-1)
 
 
-@pytest.mark.parametrize("src", [F32, BF16, MXFP4], ids=["f32", "bf16", "mxfp4"])
+@pytest.mark.parametrize("src", [F32, F16, BF16, Q8_0, MXFP4], ids=["f32", "f16", "bf16", "q8_0", "mxfp4"])
 @pytest.mark.parametrize("typ", ALL, ids=[NAMES[t] for t in ALL])
 def test_requantize_dev_matches_oracle(env, oracle_lib, typ, src):
     torch, gq = env
@@ -92,7 +93,9 @@ def test_device_api_argument_checks(env):
     out = torch.zeros(4096, dtype=torch.uint8, device="cuda")
     im = torch.ones(512, dtype=torch.float32, device="cuda")
     p = raw.data_ptr()
-    assert gq.gpuq_requantize_dev(F16, p, 12, out.data_ptr(), 1, 4, 512, None, st) == 0       # F16 is not fused
+    assert gq.gpuq_requantize_dev(F16, p + 2, 12, out.data_ptr(), 1, 4, 512, None, st) == 0   # unaligned source
+    assert gq.gpuq_requantize_dev(Q8_0, p + 1, 12, out.data_ptr(), 1, 4, 512, None, st) == 0  # odd Q8_0 blocks
+    assert gq.gpuq_requantize_dev(2, p, 12, out.data_ptr(), 1, 4, 512, None, st) == 0         # unknown source
     assert gq.gpuq_requantize_dev(F32, p + 4, 12, out.data_ptr(), 1, 4, 512, None, st) == 0   # unaligned source
     assert gq.gpuq_requantize_dev(F32, p, 16, out.data_ptr(), 1, 4, 512, None, st) == 0       # IQ2_XXS: imatrix
     assert gq.gpuq_requantize_dev(F32, p, 12, out.data_ptr(), 1, 4, 500, None, st) == 0       # row not in blocks
@@ -101,3 +104,50 @@ def test_device_api_argument_checks(env):
     assert gq.gpuq_dequantize_src_dev(7, p, out.data_ptr(), 64, st) == 0                      # unknown source
     torch.cuda.synchronize()
     assert gq.gpuq_take_error() == 0
+
+
+KQ = [10, 11, 12, 13, 14]
+
+
+@pytest.mark.parametrize("typ", KQ, ids=[NAMES[t] for t in KQ])
+def test_dequantize_dev_kquants_match_oracle(env, oracle_lib, typ):
+    """ggml's to_float of the k-quants on the device, bit for bit against the oracle's (both imatrix modes' bytes,
+    zero and subnormal blocks included)"""
+    torch, gq = env
+    rng = np.random.default_rng(typ + 7)
+    x = (rng.standard_normal((12, 1024)) * rng.uniform(0.005, 0.05, (12, 1))).astype(np.float32)
+    x[0] = 0
+    x[1] *= 1e-20
+    im = rng.lognormal(0.0, 1.5, 1024).astype(np.float32)
+    q = np.concatenate([oracle_lib.quantize(typ, x, None).reshape(-1), oracle_lib.quantize(typ, x, im).reshape(-1)])
+    nblk = q.size // gq.gpuq_block_bytes(typ)
+    want = oracle_lib.dequantize(typ, q, nblk * 256)
+    d_q = torch.from_numpy(q).cuda()
+    d_out = torch.empty(nblk * 256, dtype=torch.float32, device="cuda")
+    print("case dequantize_dev %s" % NAMES[typ], flush=True)
+    assert gq.gpuq_can_dequantize_type(typ) == 1
+    got = gq.gpuq_dequantize_dev(typ, d_q.data_ptr(), d_out.data_ptr(), nblk, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert got == nblk * 256 * 4
+    assert np.array_equal(d_out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+def test_synthetic_tables_need_the_opt_in(env):
+    """a table file with the stand-in mark loads its IQ tables only under GPUQ_ALLOW_SYNTHETIC_TABLES=1: without it
+    the IQ1/IQ2/IQ3 types report unavailable and the rest still work; the opt-in restores them"""
+    import os
+    import gpuq
+    torch, gq = env
+    path = gpuq.tables_path().encode()
+    old = os.environ.pop("GPUQ_ALLOW_SYNTHETIC_TABLES", None)
+    try:
+        print("case tables without the opt-in", flush=True)
+        assert gq.gpuq_init(path, 0) == 0
+        assert [gq.gpuq_can_quantize(t, 1) for t in (16, 17, 18, 19, 21, 22, 29)] == [0] * 7
+        assert [gq.gpuq_can_dequantize_type(t) for t in (16, 19, 29)] == [0] * 3
+        assert [gq.gpuq_can_quantize(t, 1) for t in (8, 12, 14, 20, 23)] == [1] * 5
+        assert gq.gpuq_can_dequantize_type(23) == 1
+    finally:
+        os.environ["GPUQ_ALLOW_SYNTHETIC_TABLES"] = old if old is not None else "1"
+        assert gq.gpuq_init(path, 0) == 0
+    assert [gq.gpuq_can_quantize(t, 1) for t in (16, 17, 18, 19, 21, 22, 29)] == [1] * 7

@@ -1,13 +1,15 @@
 """The on-device LDLQ loop (gpuq_ldlq_dev) against the CPU oracle's fixed-order loop, byte for byte, on the recipe
 of the reference's tools/test_ldlq.py:42-50 (a correlated Gaussian design, H = X^T X in f64, imatrix = diag(H)/n,
 W ~ N(0, 0.05)), in sequential and act order, with a shared and with per-matrix factors, and without feedback
-(where it must equal plain quantization, tools/test_ldlq.py:69-73)."""
+(where it must equal plain quantization, tools/test_ldlq.py:69-73); i-quant and k-quant targets; the three
+importance modes of tools/ldlq.py:88-96 (imatrix, diag, schur); calls from two streams ordered on the device."""
 import numpy as np
 import pytest
 
 pytestmark = pytest.mark.gpu
 
-TYPES = {22: "iq2_s", 16: "iq2_xxs", 19: "iq1_s", 29: "iq1_m", 23: "iq4_xs", 18: "iq3_xxs"}
+TYPES = {22: "iq2_s", 16: "iq2_xxs", 19: "iq1_s", 29: "iq1_m", 23: "iq4_xs", 18: "iq3_xxs", 12: "q4_k", 13: "q5_k",
+         14: "q6_k"}
 
 
 @pytest.fixture(scope="module")
@@ -143,7 +145,7 @@ def test_ldlq_host_matches_oracle(env, oracle_lib, typ, shared):
     Hh = np.ascontiguousarray(H if shared else np.stack([H, H2]), dtype=np.float64)
     print("case ldlq host %d shared=%s" % (typ, shared), flush=True)
     got = gq.gpuq_ldlq(typ, np.ascontiguousarray(W).ctypes.data, Hh.ctypes.data, 0 if shared else 768 * 768,
-                       float(n), 0.01, 1, ims.ctypes.data, 2, 32, 768, out.ctypes.data)
+                       float(n), 0.01, 1, 0, ims.ctypes.data, 2, 32, 768, out.ctypes.data)
     assert got == out.nbytes
     assert np.array_equal(out, want), "%d bytes differ" % int((out != want).sum())
 
@@ -181,3 +183,64 @@ def test_hessian_accumulate_dev(env):
     assert np.array_equal(H, H.T)
     assert np.allclose(H, want, rtol=1e-12, atol=1e-12 * np.abs(want).max())
     assert gq.gpuq_hessian_accumulate_dev(dX.data_ptr(), nrows, 500, dH.data_ptr(), st) == 1
+
+
+def test_schur_weights_dev_matches_oracle(env, oracle_lib):
+    """gpuq_schur_weights_dev == the oracle's fixed-order restatement, bit for bit, in every row it fills"""
+    torch, gpuq, gq = env
+    from gpuq import ldlq
+    H, n, _, _ = design(ne1=8, ne0=1024)
+    U, perm, diag_n, _ = ldlq.prepare_hessian(H, n, damp=0.01, order="act")
+    want = oracle_lib.schur_weights(U)
+    print("case schur_weights_dev", flush=True)
+    got = ldlq.schur_weights_dev(gq, torch.from_numpy(U).cuda(), nrep=3)
+    torch.cuda.synchronize()
+    g = got.cpu().numpy()
+    for r in range(3):
+        assert np.array_equal(g[r].view(np.uint32), want.view(np.uint32))
+    assert np.allclose(want, ldlq.block_weights("schur", U=U, perm=perm, diag_n=diag_n), rtol=2e-6)
+
+
+@pytest.mark.parametrize("weights", ["diag", "schur"])
+@pytest.mark.parametrize("typ", [22, 12], ids=["iq2_s", "q4_k"])
+def test_ldlq_host_weight_modes(env, oracle_lib, typ, weights):
+    """gpuq_ldlq with the importance from the Hessian (diag(H)/n) or the factor (schur) == the oracle's loop on the
+    device-built factor with the same importances"""
+    torch, gpuq, gq = env
+    from gpuq import ldlq
+    H, n, _, W = design(ne1=32, ne0=768)
+    U, perm, diag_n, _ = prepare_dev(torch, gq, H, n, "act")
+    qw = diag_n.astype(np.float32) if weights == "diag" else oracle_lib.schur_weights(U)
+    want = np.stack([oracle_lib.ldlq(typ, W[m:m + 1][:, :, perm], U, qw[None], ldlq.slot_order(perm))[0][0]
+                     for m in range(2)])
+    print("case ldlq host %d weights=%s" % (typ, weights), flush=True)
+    got = ldlq.quantize_matrix_host(gq, typ, W, H, n, None, order="act", weights=weights)
+    assert np.array_equal(got, want), "%d bytes differ" % int((got != want).sum())
+
+
+def test_ldlq_calls_from_two_streams_are_ordered(env, oracle_lib):
+    """two gpuq_ldlq_dev calls issued back to back on different streams share the library's Es scratch: the second
+    waits for the first on the device, so each equals the oracle's loop"""
+    torch, gpuq, gq = env
+    from gpuq import ldlq
+    H, n, imatrix, W = design(ne1=256, ne0=1024)
+    U, perm, _, _ = ldlq.prepare_hessian(H, n, damp=0.01, order="seq")
+    slots = np.ascontiguousarray(ldlq.slot_order(perm), dtype=np.int64)
+    qw = np.stack([imatrix[perm]] * 2).astype(np.float32)
+    want = oracle_lib.ldlq(22, W[:, :, perm], U, qw, slots)[0]
+    dU = torch.from_numpy(U).cuda()
+    dqw = torch.from_numpy(qw).cuda()
+    Wp = torch.from_numpy(np.ascontiguousarray(W[:, :, perm])).cuda()
+    parts = [Wp[m:m + 1].clone() for m in range(2)]
+    outs = [torch.empty((1, 256, 4 * 82), dtype=torch.uint8, device="cuda") for _ in range(2)]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    print("case ldlq two streams", flush=True)
+    for m in range(2):
+        got = gq.gpuq_ldlq_dev(22, parts[m].data_ptr(), dU.data_ptr(), 0, dqw[m].data_ptr(), 1, 256, 1024,
+                               slots.ctypes.data, 1, outs[m].data_ptr(), streams[m].cuda_stream)
+        assert got == outs[m].numel()
+    torch.cuda.synchronize()
+    for m in range(2):
+        assert np.array_equal(outs[m].cpu().numpy()[0], want[m])
+    assert gq.gpuq_take_error() == 0

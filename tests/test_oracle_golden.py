@@ -2,13 +2,14 @@
 compiled from its own source into oracle/_ref/ and run on an MI355X by tests/golden/make_ref_golden.py over a row
 subset of the reference's self-test fixture (gpuq/test_gpuq.py:57-73), with this repository's search tables.
 Every type and imatrix mode must match byte for byte, and the i-quant dequantizers bit for bit (sha256)."""
-import hashlib
 import os
 
 import numpy as np
 import pytest
 
 from conftest import TABLES
+
+import tables
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 GOLDEN = os.path.join(HERE, "golden", "ref_vectors.npz")
@@ -22,7 +23,7 @@ def golden():
     g = np.load(GOLDEN, allow_pickle=False)
     xs, ims = golden_inputs()
     assert str(g["meta_inputs"]) == sha(np.stack(xs)) + sha(np.stack(ims)), "fixture inputs changed"
-    assert str(g["meta_tables"]) == hashlib.sha256(open(TABLES, "rb").read()).hexdigest(), "tables changed"
+    assert str(g["meta_tables"]) == tables.content_sha(TABLES), "tables changed"
     return g, xs, ims, sha
 
 

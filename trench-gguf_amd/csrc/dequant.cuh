@@ -1,8 +1,10 @@
-// trench-gguf_amd/csrc/dequant.cuh - ggml's to_float of the i-quants and IQ4_XS, and the source decoder.
+// trench-gguf_amd/csrc/dequant.cuh - ggml's to_float of the i-quants, IQ4_XS and the k-quants, and the source decoder.
 //
-// Semantics: dequantize_row_iq* (gpuq/gpuq.hip:1850-2021): only products of small integers, fp16 scales and powers
-// of two, in ggml's operand order, so fp32 reproduces ggml bit for bit. One thread produces one 32-value chunk
-// (8 threads a super-block) with 16-byte stores; the dequantizer grid (uint64 points) is read through the cache.
+// Semantics: dequantize_row_iq* (gpuq/gpuq.hip:1850-2021) and ggml's dequantize_row_q2_K .. q6_K (the reference
+// reads the k-quants back through libggml-base's to_float, tools/requant_experts.py:588-591): only products of small
+// integers, fp16 scales and powers of two, in ggml's operand order, so fp32 reproduces ggml bit for bit. One thread
+// produces one 32-value chunk (8 threads a super-block) with 16-byte stores; the dequantizer grid (uint64 points) is
+// read through the cache.
 #pragma once
 #include "common.cuh"
 
@@ -14,6 +16,18 @@ DEV uint32_t rd32u(const uint8_t *p) { return rd16(p) | (rd16(p + 2) << 16); }  
 DEV uint32_t gbyte(uint64_t pt, int j) { return (uint32_t)(pt >> (8 * j)) & 0xffu; }
 
 __constant__ int8_t k_iq4nl_i8[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+// Q4_K / Q5_K: sub-block j's 6-bit scale and min from the 12-byte scales field (j < 4: low 6 bits of bytes j and j+4;
+// j >= 4: a nibble of byte j+4 and the top 2 bits of bytes j-4 and j)
+DEV void k4_scale_min(const uint8_t *s, int j, uint32_t &sc, uint32_t &mn) {
+    if (j < 4) {
+        sc = rd8(s + j) & 63;
+        mn = rd8(s + j + 4) & 63;
+    } else {
+        sc = (rd8(s + j + 4) & 0xf) | ((rd8(s + j - 4) >> 6) << 4);
+        mn = (rd8(s + j + 4) >> 4) | ((rd8(s + j) >> 6) << 4);
+    }
+}
 
 template <int TYPE> DEV void dq_chunk(const uint8_t *x, int ib, float (&y)[32], const uint64_t *grid) {
     if (TYPE == T_IQ2_XXS) {
@@ -124,6 +138,67 @@ template <int TYPE> DEV void dq_chunk(const uint8_t *x, int ib, float (&y)[32], 
             const uint32_t q = rd8(x + 8 + 16 * ib + j);
             y[j] = dl * k_iq4nl_i8[q & 0xf];
             y[j + 16] = dl * k_iq4nl_i8[q >> 4];
+        }
+    } else if (TYPE == T_Q4_K || TYPE == T_Q5_K) {
+        // block d dmin scales[12] (qh[32], Q5_K) qs[128]; chunk ib: sub-block ib's 6-bit scale and min, the low
+        // (even ib) or high (odd ib) nibbles of qs[32 (ib/2) ..], Q5_K's fifth bit from bit ib of qh[j]
+        const float d = h2f(rd16(x)), dmin = h2f(rd16(x + 2));
+        uint32_t sc, mn;
+        k4_scale_min(x + 4, ib, sc, mn);
+        const float dl = d * (float)sc, ml = dmin * (float)mn;
+        const uint8_t *q = x + (TYPE == T_Q5_K ? 48 : 16) + 32 * (ib / 2);
+        const int sh = 4 * (ib & 1);
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            int v = (int)((rd8(q + j) >> sh) & 0xf);
+            if (TYPE == T_Q5_K) v += (rd8(x + 16 + j) >> ib) & 1 ? 16 : 0;
+            y[j] = dl * (float)v - ml;
+        }
+    } else if (TYPE == T_Q6_K) {
+        // block ql[128] qh[64] scales[16] (int8) d; chunk ib = 4n + part of the 128-value half n: ql[64n + 32 (part
+        // & 1) + j], its low (part < 2) or high nibble, bits 2 part of qh[32n + j], scale scales[8n + 2 part + j/16]
+        const float d = h2f(rd16(x + 208));
+        const int n = ib / 4, part = ib % 4;
+        const uint8_t *ql = x + 64 * n + 32 * (part & 1), *qh = x + 128 + 32 * n;
+        const int qsh = 4 * (part >> 1), hsh = 2 * part;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            const int q = (int)(((rd8(ql + j) >> qsh) & 0xf) | (((rd8(qh + j) >> hsh) & 3) << 4)) - 32;
+            const int s = (int)(int8_t)rd8(x + 192 + 8 * n + 2 * part + j / 16);
+            y[j] = d * (float)s * (float)q;
+        }
+    } else if (TYPE == T_Q2_K) {
+        // block scales[16] qs[64] d dmin; chunk ib = 4n + j: 2-bit fields at shift 2j of qs[32n + 16h + l], scale
+        // byte 8n + 2j + h (low nibble the scale, high the min) for its halves h
+        const float d = h2f(rd16(x + 80)), dmin = h2f(rd16(x + 82));
+        const int n = ib / 4, jj = ib % 4;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t sc = rd8(x + 8 * n + 2 * jj + h);
+            const float dl = d * (float)(sc & 0xf), ml = dmin * (float)(sc >> 4);
+#pragma unroll
+            for (int l = 0; l < 16; ++l)
+                y[16 * h + l] = dl * (float)((rd8(x + 16 + 32 * n + 16 * h + l) >> (2 * jj)) & 3) - ml;
+        }
+    } else if (TYPE == T_Q3_K) {
+        // block hmask[32] qs[64] scales[12] d; chunk ib = 4n + j: 2-bit fields at shift 2j of qs[32n + 16h + l],
+        // minus 4 where bit 4n + j of hmask[16h + l] is clear; 6-bit scale 8n + 2j + h (low 4 bits from a nibble of
+        // scales[0..7], high 2 bits from scales[8..11]), minus 32
+        const float d = h2f(rd16(x + 108));
+        const int n = ib / 4, jj = ib % 4;
+        const uint8_t *s = x + 96;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int i = 8 * n + 2 * jj + h;
+            const uint32_t lo = i < 8 ? rd8(s + i) & 0xf : rd8(s + i - 8) >> 4;
+            const int sc = (int)(lo | (((rd8(s + 8 + i % 4) >> (2 * (i / 4))) & 3) << 4)) - 32;
+            const float dl = d * (float)sc;
+#pragma unroll
+            for (int l = 0; l < 16; ++l) {
+                const int q = (int)((rd8(x + 32 + 32 * n + 16 * h + l) >> (2 * jj)) & 3) -
+                              ((rd8(x + 16 * h + l) >> (4 * n + jj)) & 1 ? 0 : 4);
+                y[16 * h + l] = dl * (float)q;
+            }
         }
     }
 }

@@ -43,6 +43,9 @@ struct Tabs {
 };
 
 Tabs g_tabs[64];
+// the record type that marks a table file holding stand-in codebooks instead of ggml's (the build's own generator
+// writes it; a file written from ggml by the reference's gpuq_tables.c has none)
+constexpr int SYNTHETIC_MARK = 0x53594e54;
 int g_device = -1;
 int g_ncu = 256;
 int *g_err = nullptr;          // device flag: a search found no candidate (the reference traps there)
@@ -178,15 +181,31 @@ template <int SRC> bool dispatch_src(int type, const QParams &p, hipStream_t st)
     }
 }
 
-// fused decode for F32 / BF16 / MXFP4 sources (the configurations' encodings); F16 and Q8_0 sources are decoded
-// to f32 by a separate pass first (exact either way)
-bool fused_src(int src) { return src == T_F32 || src == T_BF16 || src == T_MXFP4; }
+// every stored source encoding is decoded in registers inside the quantize kernel (SrcLoad in common.cuh)
+bool fused_src(int src) {
+    return src == T_F32 || src == T_F16 || src == T_BF16 || src == T_Q8_0 || src == T_MXFP4;
+}
 
 bool dispatch(int type, int src, const QParams &p, hipStream_t st) {
     switch (src) {
         case T_F32: return dispatch_src<T_F32>(type, p, st);
+        case T_F16: return dispatch_src<T_F16>(type, p, st);
         case T_BF16: return dispatch_src<T_BF16>(type, p, st);
+        case T_Q8_0: return dispatch_src<T_Q8_0>(type, p, st);
         case T_MXFP4: return dispatch_src<T_MXFP4>(type, p, st);
+        default: return false;
+    }
+}
+
+// the source pointer alignment and row length the fused loads need: F32 / F16 / BF16 read 16 bytes a load (base and
+// row starts 16-byte aligned), Q8_0 16-bit words (2-byte blocks), MXFP4 bytes
+bool src_aligned(int src, const void *raw, int64_t n_per_row) {
+    const uintptr_t a = (uintptr_t)raw;
+    switch (src) {
+        case T_F32: return (a & 15) == 0 && (n_per_row * 4) % 16 == 0;
+        case T_F16: case T_BF16: return (a & 15) == 0 && (n_per_row * 2) % 16 == 0;
+        case T_Q8_0: return (a & 1) == 0;
+        case T_MXFP4: return true;
         default: return false;
     }
 }
@@ -287,7 +306,7 @@ struct PinBuf {
 
 constexpr int NSLOT = 3;
 struct Slot {
-    Buf in, f32, out;                 // device: source bytes, decoded floats (F16 / Q8_0 sources), blocks
+    Buf in, out;                      // device: source bytes, blocks
     PinBuf pin_in, pin_out;
     hipEvent_t copied = nullptr;      // the slot's H2D copy is done: pin_in may be refilled
     hipEvent_t quantized = nullptr;   // the slot's kernels are done: in and f32 may be refilled, out is complete
@@ -365,12 +384,10 @@ size_t quantize_host(int src, const void *raw, int type, void *dst, int64_t nmat
         return std::min(r1, rows);
     };
     const int64_t max_rows = std::min(rows, std::max<int64_t>(1, budget / row_src));
-    const bool decode = !fused_src(src);
     for (Slot &s : g_slot) {
         if (!s.in.grow((size_t)(max_rows * row_src) + 16) || !s.out.grow((size_t)(max_rows * row_out) + 16) ||
             !s.pin_in.grow((size_t)(max_rows * row_src)) || !s.pin_out.grow((size_t)(max_rows * row_out)))
             return 0;
-        if (decode && !s.f32.grow((size_t)(max_rows * n_per_row * 4))) return 0;
         s.used = false;
     }
     const float *qw = nullptr;
@@ -401,15 +418,13 @@ size_t quantize_host(int src, const void *raw, int type, void *dst, int64_t nmat
         if (s.used) ok = hipStreamWaitEvent(g_st_in, s.quantized, 0) == hipSuccess;
         ok = ok && hipMemcpyAsync(s.in.p, s.pin_in.p, in_bytes, hipMemcpyHostToDevice, g_st_in) == hipSuccess &&
              hipEventRecord(s.copied, g_st_in) == hipSuccess;
-        // decode and quantize, once the bytes are in and the slot's previous blocks have left
+        // quantize (the source decoded in registers), once the bytes are in and the slot's previous blocks have left
         ok = ok && hipStreamWaitEvent(g_st_q, s.copied, 0) == hipSuccess;
         if (ok && s.used) ok = hipStreamWaitEvent(g_st_q, s.returned, 0) == hipSuccess;
-        const void *qsrc = decode ? s.f32.p : s.in.p;
-        if (ok && decode) ok = launch_decode(src, s.in.p, (float *)s.f32.p, cr * n_per_row, g_st_q);
         if (ok) {
             const float *cqw = qw ? qw + (r0 / nrow) * n_per_row : nullptr;
-            const QParams p = params_for(type, qsrc, s.out.p, cr * nb_row, cqw, nb_mat, nb_row, 1);
-            ok = dispatch(type, decode ? T_F32 : src, p, g_st_q) && hipEventRecord(s.quantized, g_st_q) == hipSuccess;
+            const QParams p = params_for(type, s.in.p, s.out.p, cr * nb_row, cqw, nb_mat, nb_row, 1);
+            ok = dispatch(type, src, p, g_st_q) && hipEventRecord(s.quantized, g_st_q) == hipSuccess;
         }
         // blocks -> pinned (the slot's previous blocks were taken out of pin_out by the last iteration)
         ok = ok && hipStreamWaitEvent(g_st_out, s.quantized, 0) == hipSuccess &&
@@ -432,15 +447,16 @@ size_t quantize_host(int src, const void *raw, int type, void *dst, int64_t nmat
     return (size_t)(rows * row_out);
 }
 
-// the LDLQ loop's side stream and its events (created once, on the library's device; default priority)
+// the LDLQ loop's side stream and its events (created once, on the library's device; default priority); g_ev_done
+// marks the end of the last gpuq_ldlq_dev call's launches (g_ldlq_pending: one was recorded)
 hipStream_t g_st2 = nullptr;
-hipEvent_t g_ev_start = nullptr, g_ev_solved = nullptr, g_ev_rest = nullptr;
+hipEvent_t g_ev_start = nullptr, g_ev_solved = nullptr, g_ev_rest = nullptr, g_ev_done = nullptr;
+bool g_ldlq_pending = false;
 bool side_stream_ready() {
     if (g_st2) return true;
-    if (hipStreamCreateWithFlags(&g_st2, hipStreamNonBlocking) != hipSuccess) return false;
-    for (hipEvent_t *e : {&g_ev_start, &g_ev_solved, &g_ev_rest})
+    for (hipEvent_t *e : {&g_ev_start, &g_ev_solved, &g_ev_rest, &g_ev_done})
         if (hipEventCreateWithFlags(e, hipEventDisableTiming) != hipSuccess) return false;
-    return true;
+    return hipStreamCreateWithFlags(&g_st2, hipStreamNonBlocking) == hipSuccess;
 }
 
 // W -= Es . U[c0 .. c0+255][cb .. ce) for every matrix
@@ -452,9 +468,11 @@ bool launch_update(float *W, const double *Es, const double *U, int64_t u_stride
     return hipGetLastError() == hipSuccess;
 }
 
+// the 256-weight types whose quantizer is closed per super-block and that have a device dequantizer (the
+// reference's LDLQ_TYPES, tools/requant_experts.py:195-196, plus Q2_K / Q3_K)
 bool ldlq_type(int t) {
     return t == T_IQ2_XXS || t == T_IQ2_XS || t == T_IQ2_S || t == T_IQ3_XXS || t == T_IQ3_S || t == T_IQ1_S ||
-           t == T_IQ1_M || t == T_IQ4_XS;
+           t == T_IQ1_M || t == T_IQ4_XS || t == T_Q2_K || t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K;
 }
 
 bool launch_solve(int type, const float *W, const uint8_t *q, int64_t q_stride, int64_t q_off, const double *U,
@@ -472,6 +490,11 @@ bool launch_solve(int type, const float *W, const uint8_t *q, int64_t q_stride, 
         case T_IQ1_S: KSOLVE(T_IQ1_S); break;
         case T_IQ1_M: KSOLVE(T_IQ1_M); break;
         case T_IQ4_XS: KSOLVE(T_IQ4_XS); break;
+        case T_Q2_K: KSOLVE(T_Q2_K); break;
+        case T_Q3_K: KSOLVE(T_Q3_K); break;
+        case T_Q4_K: KSOLVE(T_Q4_K); break;
+        case T_Q5_K: KSOLVE(T_Q5_K); break;
+        case T_Q6_K: KSOLVE(T_Q6_K); break;
         default: return false;
     }
 #undef KSOLVE
@@ -507,15 +530,30 @@ extern "C" int gpuq_init(const char *tables, int device) {
     }
     fclose(f);
     // validate everything before touching the device tables
+    bool synthetic = false;
     for (const Rec &r : recs) {
-        if (r.type >= 1000) {
+        if (r.type == SYNTHETIC_MARK) {
+            synthetic = true;
+        } else if (r.type >= 1000) {
             const int t = r.type - 1000;
             if (t < 0 || t >= 64 || !is_search_type(t) || (int)r.grid.size() != expected_grid(t)) return 6;
         } else if (r.type >= 0 && r.type < 64 && is_search_type(r.type)) {
             if (!valid_search(r.type, r.grid, r.map, r.neigh)) return 6;
         }
     }
+    // the tables of an earlier call are replaced (once no launch can read them any more)
+    if (hipDeviceSynchronize() != hipSuccess) return 4;
+    for (Tabs &t : g_tabs) {
+        for (void *p : {(void *)t.grid, (void *)t.map, (void *)t.map3, (void *)t.neigh, (void *)t.dq})
+            if (p) (void)hipFree(p);
+        t = Tabs();
+    }
+    // stand-in codebooks (the file carries the mark) are loaded only where the caller asks for them: quantizing
+    // with them writes grid indices llama.cpp would read against ggml's own grids
+    const char *allow = getenv("GPUQ_ALLOW_SYNTHETIC_TABLES");
+    if (synthetic && !(allow && allow[0] == '1')) recs.clear();
     for (const Rec &r : recs) {
+        if (r.type == SYNTHETIC_MARK) continue;
         if (r.type >= 1000) {
             Tabs &t = g_tabs[r.type - 1000];
             if (!upload(&t.dq, r.grid)) return 4;
@@ -611,7 +649,8 @@ extern "C" int gpuq_can_dequantize_type(int type) {
     switch (type) {
         case T_IQ2_XXS: case T_IQ2_XS: case T_IQ2_S: case T_IQ3_XXS: case T_IQ3_S: case T_IQ1_S: case T_IQ1_M:
             return g_device >= 0 && tab_of(type).dq != nullptr;
-        case T_IQ4_XS: return g_device >= 0 ? 1 : 0;
+        case T_IQ4_XS: case T_Q2_K: case T_Q3_K: case T_Q4_K: case T_Q5_K: case T_Q6_K:
+            return g_device >= 0 ? 1 : 0;
         default: return 0;
     }
 }
@@ -632,6 +671,11 @@ extern "C" size_t gpuq_dequantize_dev(int type, const void *d_q, float *d_out, i
         case T_IQ1_S: KDQ(T_IQ1_S, 50); break;
         case T_IQ1_M: KDQ(T_IQ1_M, 56); break;
         case T_IQ4_XS: KDQ(T_IQ4_XS, 136); break;
+        case T_Q2_K: KDQ(T_Q2_K, 84); break;
+        case T_Q3_K: KDQ(T_Q3_K, 110); break;
+        case T_Q4_K: KDQ(T_Q4_K, 144); break;
+        case T_Q5_K: KDQ(T_Q5_K, 176); break;
+        case T_Q6_K: KDQ(T_Q6_K, 210); break;
         default: return 0;
     }
 #undef KDQ
@@ -647,13 +691,14 @@ extern "C" size_t gpuq_dequantize_src_dev(int src, const void *d_raw, float *d_o
 }
 
 // Device-pointer requantize (no counterpart in the reference): nmat matrices of nrow x n_per_row values stored as
-// src (F32 / BF16 / MXFP4 decoded in registers inside the quantize kernel) -> d_dst, matrix m weighted by
-// d_imatrix + m * n_per_row (or no imatrix). Asynchronous on `stream`. Returns the bytes the launch will write.
+// src (F32 / F16 / BF16 / Q8_0 / MXFP4, decoded in registers inside the quantize kernel) -> d_dst, matrix m
+// weighted by d_imatrix + m * n_per_row (or no imatrix). Asynchronous on `stream`. Returns the bytes the launch will
+// write.
 extern "C" size_t gpuq_requantize_dev(int src, const void *d_raw, int type, void *d_dst, int64_t nmat, int64_t nrow,
                                       int64_t n_per_row, const float *d_imatrix, void *stream) {
     if (nmat <= 0 || nrow <= 0 || !fused_src(src) || !type_ok(type, n_per_row, d_imatrix != nullptr)) return 0;
-    if (((uintptr_t)d_raw & 15) || (d_imatrix && ((uintptr_t)d_imatrix & 15)) || ((uintptr_t)d_dst & 1)) return 0;
-    if ((n_per_row * (src == T_F32 ? 4 : 2)) % 16 && src != T_MXFP4) return 0;
+    if (n_per_row % 32 || !src_aligned(src, d_raw, n_per_row)) return 0;
+    if ((d_imatrix && ((uintptr_t)d_imatrix & 15)) || ((uintptr_t)d_dst & 1)) return 0;
     const int bs = block_len(type);
     const int64_t nb_row = n_per_row / bs, nb_mat = nrow * nb_row, nunits = nmat * nb_mat;
     const QParams p = params_for(type, d_raw, d_dst, nunits, d_imatrix, nb_mat, nb_row, 1);
@@ -678,28 +723,34 @@ extern "C" int gpuq_take_error(void) {
 // factor of the permuted inverse Hessian, [ne0][ne0] f64 row-major, matrix m's at d_u + m*u_stride (0: shared);
 // d_qw: [nmat][ne0] f32 importances in permuted order; blk_order (host, ne0/256 entries): the output slot of permuted
 // block k; d_out: [nmat][ne1][ne0/256 blocks]. feedback = 0 quantizes every block as is. Asynchronous on `stream`.
-extern "C" size_t gpuq_ldlq_dev(int type, float *d_wp, const double *d_u, int64_t u_stride, const float *d_qw,
-                                int64_t nmat, int64_t ne1, int64_t ne0, const int64_t *blk_order, int feedback,
-                                void *d_out, void *stream) {
-    if (!ldlq_type(type) || !gpuq_can_dequantize_type(type) || !type_ok(type, ne0, d_qw != nullptr)) return 0;
-    if (nmat <= 0 || ne1 <= 0 || ne0 <= 0 || ne0 % QK || u_stride < 0 || !blk_order) return 0;
+namespace {
+
+// the argument checks both LDLQ entry points share
+bool ldlq_args_ok(int type, const float *d_wp, const double *d_u, int64_t u_stride, const float *d_qw, int64_t nmat,
+                  int64_t ne1, int64_t ne0, const int64_t *blk_order, const void *d_out) {
+    if (!ldlq_type(type) || !gpuq_can_dequantize_type(type) || !type_ok(type, ne0, d_qw != nullptr)) return false;
+    if (nmat <= 0 || ne1 <= 0 || ne0 <= 0 || ne0 % QK || u_stride < 0 || !blk_order) return false;
     if (((uintptr_t)d_wp & 15) || (d_qw && ((uintptr_t)d_qw & 15)) || ((uintptr_t)d_u & 7) || ((uintptr_t)d_out & 1))
-        return 0;
+        return false;
     const int64_t nblk = ne0 / QK;
     for (int64_t k = 0; k < nblk; ++k)
-        if (blk_order[k] < 0 || blk_order[k] >= nblk) return 0;
-    const hipStream_t st = (hipStream_t)stream;
-    const int64_t bb = (int64_t)gpuq_block_bytes(type), rows = nmat * ne1;
-    std::lock_guard<std::mutex> lock(g_mu);
-    const bool fb = feedback && nblk > 1;
-    // Es of two consecutive blocks (the update of block k's later columns still reads Es(k) while Es(k+1) is solved)
-    if (fb && (!g_es.grow((size_t)2 * rows * QK * 8) || !side_stream_ready())) return 0;
-    // Block k's update is split: the next block's 256 columns on the caller's stream (they gate quantizing block
-    // k+1), the rest on a side stream, where it runs alongside block k+1's quantization and solve. Every column still
-    // receives its updates in block order: the next-block part of update k waits for the side stream's update k-1.
-    if (fb) {
+        if (blk_order[k] < 0 || blk_order[k] >= nblk) return false;
+    return true;
+}
+
+// The loop's launches on `st`, with es holding two blocks of Es (2 * rows * 256 doubles; the update of block k's
+// later columns still reads Es(k) while Es(k+1) is solved). side: block k's update is split, the next block's 256
+// columns on `st` (they gate quantizing block k+1) and the rest on the library's side stream, where it runs beside
+// block k+1's quantization and solve; every column still receives its updates in block order (the next-block part of
+// update k waits for the side stream's update k-1), and `st` joins the side stream at the end. Without side, every
+// launch is on `st`. Launches only: allocates nothing.
+bool ldlq_loop(int type, float *d_wp, const double *d_u, int64_t u_stride, const float *d_qw, int64_t nmat,
+               int64_t ne1, int64_t ne0, const int64_t *blk_order, bool fb, void *d_out, hipStream_t st, double *es2,
+               bool side) {
+    const int64_t nblk = ne0 / QK, bb = (int64_t)gpuq_block_bytes(type), rows = nmat * ne1;
+    if (fb && side) {
         if (hipEventRecord(g_ev_start, st) != hipSuccess || hipStreamWaitEvent(g_st2, g_ev_start, 0) != hipSuccess)
-            return 0;
+            return false;
     }
     bool rest_pending = false;      // a side-stream update not yet waited for by the caller's stream
     for (int64_t k = 0; k < nblk; ++k) {
@@ -711,30 +762,55 @@ extern "C" size_t gpuq_ldlq_dev(int type, float *d_wp, const double *d_u, int64_
         p.qw_off = c0;
         p.out_stride = nblk * bb;
         p.out_off = blk_order[k] * bb;
-        if (!dispatch(type, T_F32, p, st)) return 0;
+        if (!dispatch(type, T_F32, p, st)) return false;
         if (!fb || k + 1 >= nblk) continue;
-        double *es = (double *)g_es.p + (size_t)(k & 1) * rows * QK;
+        double *es = es2 + (size_t)(k & 1) * rows * QK;
         if (!launch_solve(type, d_wp, (const uint8_t *)d_out, nblk * bb, blk_order[k] * bb, d_u, u_stride, nmat, ne1,
                           ne0, c0, es, st))
-            return 0;
-        if (hipEventRecord(g_ev_solved, st) != hipSuccess) return 0;
-        if (rest_pending) {
-            if (hipStreamWaitEvent(st, g_ev_rest, 0) != hipSuccess) return 0;
-            rest_pending = false;
+            return false;
+        const int64_t cn = side && c0 + 2 * QK < ne0 ? c0 + 2 * QK : ne0;
+        if (side) {
+            if (hipEventRecord(g_ev_solved, st) != hipSuccess) return false;
+            if (rest_pending) {
+                if (hipStreamWaitEvent(st, g_ev_rest, 0) != hipSuccess) return false;
+                rest_pending = false;
+            }
         }
-        const int64_t cn = c0 + 2 * QK < ne0 ? c0 + 2 * QK : ne0;
-        if (!launch_update(d_wp, es, d_u, u_stride, nmat, ne1, ne0, c0, c0 + QK, cn, st)) return 0;
+        if (!launch_update(d_wp, es, d_u, u_stride, nmat, ne1, ne0, c0, c0 + QK, cn, st)) return false;
         if (cn < ne0) {
             if (hipStreamWaitEvent(g_st2, g_ev_solved, 0) != hipSuccess ||
                 !launch_update(d_wp, es, d_u, u_stride, nmat, ne1, ne0, c0, cn, ne0, g_st2) ||
                 hipEventRecord(g_ev_rest, g_st2) != hipSuccess)
-                return 0;
+                return false;
             rest_pending = true;
         }
     }
-    if (fb) {       // the caller's stream joins the side stream
+    if (fb && side) {   // the caller's stream joins the side stream
         if (hipEventRecord(g_ev_rest, g_st2) != hipSuccess || hipStreamWaitEvent(st, g_ev_rest, 0) != hipSuccess)
-            return 0;
+            return false;
+    }
+    return true;
+}
+
+}  // namespace
+
+extern "C" size_t gpuq_ldlq_dev(int type, float *d_wp, const double *d_u, int64_t u_stride, const float *d_qw,
+                                int64_t nmat, int64_t ne1, int64_t ne0, const int64_t *blk_order, int feedback,
+                                void *d_out, void *stream) {
+    if (!ldlq_args_ok(type, d_wp, d_u, u_stride, d_qw, nmat, ne1, ne0, blk_order, d_out)) return 0;
+    const hipStream_t st = (hipStream_t)stream;
+    const int64_t nblk = ne0 / QK, bb = (int64_t)gpuq_block_bytes(type), rows = nmat * ne1;
+    std::lock_guard<std::mutex> lock(g_mu);
+    const bool fb = feedback && nblk > 1;
+    if (fb && (!g_es.grow((size_t)2 * rows * QK * 8) || !side_stream_ready())) return 0;
+    // calls share Es and the side stream: each call's launches wait for the previous call's (on whatever stream it
+    // ran), so calls from several streams never run over each other's Es
+    if (fb && g_ldlq_pending && hipStreamWaitEvent(st, g_ev_done, 0) != hipSuccess) return 0;
+    if (!ldlq_loop(type, d_wp, d_u, u_stride, d_qw, nmat, ne1, ne0, blk_order, fb, d_out, st, (double *)g_es.p, true))
+        return 0;
+    if (fb) {
+        if (hipEventRecord(g_ev_done, st) != hipSuccess) return 0;
+        g_ldlq_pending = true;
     }
     return (size_t)(rows * nblk * bb);
 }
@@ -887,16 +963,33 @@ extern "C" int gpuq_prepare_hessian_dev(const double *d_H, int64_t ne0, double n
     return 0;
 }
 
-// The LDLQ loop from host memory, with no framework on the caller's side (tools/ldlq.py:71-107 of the reference with
-// weights = "imatrix" and the factor from prepare_hessian): W [nmat][ne1][ne0] f32 (original column order), H the
-// Hessian sum over n inputs, [ne0][ne0] f64, one for all matrices (h_stride 0) or one a matrix (h_stride ne0*ne0),
-// imatrix [nmat][ne0] (NULL only for a type that takes none). Writes the GGUF bytes of every matrix to dst and returns
-// their count, or 0 on an error (a factor that cannot be built included).
+// The 'schur' importance of every 256-column block of a factor (tools/ldlq.py:90-93; no single counterpart symbol in
+// the reference, which computes it in numpy or torch): d_u [ne0][ne0] f64 upper factor (device) -> d_w [nrep][ne0]
+// f32 (device), the same ne0 values in each of the nrep rows. Fixed summation order (k_schur_weights). Asynchronous
+// on `stream`. Returns 0, 1 for bad arguments, 4 on a HIP error.
+extern "C" int gpuq_schur_weights_dev(const double *d_u, int64_t ne0, float *d_w, int64_t nrep, void *stream) {
+    if (g_device < 0 || !d_u || !d_w || ne0 <= 0 || ne0 % QK || ne0 > 65535 * (int64_t)QK || nrep <= 0) return 1;
+    if (((uintptr_t)d_u & 7) || ((uintptr_t)d_w & 3)) return 1;
+    hipLaunchKernelGGL(k_schur_weights, dim3(QK, (unsigned)(ne0 / QK)), dim3(64), 0, (hipStream_t)stream, d_u, ne0,
+                       d_w, nrep);
+    return hipGetLastError() == hipSuccess ? 0 : 4;
+}
+
+// The LDLQ loop from host memory, with no framework on the caller's side (tools/ldlq.py:71-107 of the reference,
+// quantize_matrix with the factor from prepare_hessian): W [nmat][ne1][ne0] f32 (original column order), H the
+// Hessian sum over n inputs, [ne0][ne0] f64, one for all matrices (h_stride 0) or one a matrix (h_stride ne0*ne0).
+// weights: the importance each block's quantizer gets, 0 'imatrix' (imatrix [nmat][ne0] permuted; NULL only for a
+// type that takes none), 1 'diag' (diag(H)/n, permuted), 2 'schur' (diag((U_BB^T U_BB)^-1) of each block). Writes
+// the GGUF bytes of every matrix to dst and returns their count, or 0 on an error (a factor that cannot be built
+// included).
 extern "C" size_t gpuq_ldlq(int type, const float *W, const double *H, int64_t h_stride, double n, double damp,
-                            int order, const float *imatrix, int64_t nmat, int64_t ne1, int64_t ne0, void *dst) {
+                            int order, int weights, const float *imatrix, int64_t nmat, int64_t ne1, int64_t ne0,
+                            void *dst) {
     if (!W || !H || !dst || nmat <= 0 || ne1 <= 0 || ne0 <= 0 || ne0 % QK) return 0;
     if (h_stride != 0 && h_stride != ne0 * ne0) return 0;
-    if (!ldlq_type(type) || !gpuq_can_dequantize_type(type) || !type_ok(type, ne0, imatrix != nullptr)) return 0;
+    if (weights < 0 || weights > 2 || (weights != 0 && imatrix)) return 0;
+    const bool with_qw = weights != 0 || imatrix;
+    if (!ldlq_type(type) || !gpuq_can_dequantize_type(type) || !type_ok(type, ne0, with_qw)) return 0;
     std::lock_guard<std::mutex> lock(g_mu_l);
     if (!g_st_l && hipStreamCreateWithFlags(&g_st_l, hipStreamNonBlocking) != hipSuccess) return 0;
     const hipStream_t st = g_st_l;
@@ -909,26 +1002,34 @@ extern "C" size_t gpuq_ldlq(int type, const float *W, const double *H, int64_t h
         return 0;
     if (hipMemsetAsync(g_err, 0, sizeof(int), st) != hipSuccess) return 0;
     std::vector<int64_t> perm((size_t)ne0), slots((size_t)nblk);
-    std::vector<float> qw(imatrix ? (size_t)gsz * ne0 : 0);
+    std::vector<double> diag_n((size_t)ne0);
+    std::vector<float> qw(weights != 2 && with_qw ? (size_t)gsz * ne0 : 0);
     const unsigned gy = (unsigned)std::min<int64_t>(gsz * ne1, 65535);
     for (int64_t m0 = 0; m0 < nmat; m0 += gsz) {
         if (hipMemcpyAsync(g_lH.p, H + (h_stride ? m0 * h_stride : 0), (size_t)ne0 * ne0 * 8, hipMemcpyHostToDevice,
                            st) != hipSuccess ||
             gpuq_prepare_hessian_dev((const double *)g_lH.p, ne0, n, damp, order, (double *)g_lU.p, perm.data(),
-                                     nullptr, nullptr, st) != 0)
+                                     diag_n.data(), nullptr, st) != 0)
             return 0;
         for (int64_t k = 0; k < nblk; ++k) slots[k] = perm[k * QK] / QK;
-        for (int64_t m = 0; m < gsz && imatrix; ++m)
-            for (int64_t c = 0; c < ne0; ++c) qw[m * ne0 + c] = imatrix[(m0 + m) * ne0 + perm[c]];
+        if (weights == 0 && imatrix) {
+            for (int64_t m = 0; m < gsz; ++m)
+                for (int64_t c = 0; c < ne0; ++c) qw[m * ne0 + c] = imatrix[(m0 + m) * ne0 + perm[c]];
+        } else if (weights == 1) {
+            for (int64_t m = 0; m < gsz; ++m)
+                for (int64_t c = 0; c < ne0; ++c) qw[m * ne0 + c] = (float)diag_n[c];
+        }
         if (hipMemcpyAsync(g_lW.p, W + m0 * ne1 * ne0, wbytes, hipMemcpyHostToDevice, st) != hipSuccess ||
             hipMemcpyAsync(g_lperm.p, perm.data(), (size_t)ne0 * 8, hipMemcpyHostToDevice, st) != hipSuccess ||
-            (imatrix && hipMemcpyAsync(g_lqw.p, qw.data(), (size_t)gsz * ne0 * 4, hipMemcpyHostToDevice, st) !=
-                            hipSuccess))
+            (!qw.empty() && hipMemcpyAsync(g_lqw.p, qw.data(), (size_t)gsz * ne0 * 4, hipMemcpyHostToDevice, st) !=
+                                hipSuccess))
+            return 0;
+        if (weights == 2 && gpuq_schur_weights_dev((const double *)g_lU.p, ne0, (float *)g_lqw.p, gsz, st) != 0)
             return 0;
         hipLaunchKernelGGL(k_gather_cols, dim3((unsigned)((ne0 + 255) / 256), gy), dim3(256), 0, st,
                            (const float *)g_lW.p, (float *)g_lWp.p, (const int64_t *)g_lperm.p, gsz * ne1, ne0);
         if (hipGetLastError() != hipSuccess) return 0;
-        if (!gpuq_ldlq_dev(type, (float *)g_lWp.p, (const double *)g_lU.p, 0, imatrix ? (const float *)g_lqw.p : nullptr,
+        if (!gpuq_ldlq_dev(type, (float *)g_lWp.p, (const double *)g_lU.p, 0, with_qw ? (const float *)g_lqw.p : nullptr,
                            gsz, ne1, ne0, slots.data(), 1, g_lout.p, st))
             return 0;
         if (hipMemcpyAsync((uint8_t *)dst + m0 * ne1 * row_bytes, g_lout.p, obytes, hipMemcpyDeviceToHost, st) !=

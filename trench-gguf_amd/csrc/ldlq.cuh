@@ -286,3 +286,48 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             }
         }
 }
+
+// ------------------------------------------------------------------ the 'schur' importance of a block's columns
+// tools/ldlq.py:90-93 (and 424-426): qw = diag((U_BB^T U_BB)^-1) of each 256-column diagonal block U_BB, which the
+// reference leaves to LAPACK (np.linalg.inv) or torch. Here the order is fixed: (U_BB^T U_BB)^-1 = X X^T with
+// X = U_BB^-1, so qw[i] is the squared norm of X's row i. The row comes from X U_BB = I by substitution along it:
+//   x_t = ((t == i ? 1 : 0) - acc_t) / U[t][t] for t = i .. 255, acc_t = sum_{s=i}^{t-1} x_s U[s][t],
+// each acc_t an fma chain over s ascending from 0.0 (kept as running sums: after x_s, acc_j = fma(x_s, U[s][j], acc_j)
+// for the later columns), and qw[i] = (float)(sum_t x_t^2), an fma chain over t ascending from 0.0.
+// One wave a row (grid: 256 rows x the blocks): lane L keeps acc for the block's columns L, L+64, L+128, L+192; row
+// t + 1 of U is read while row t is used. Columns at or before t are updated too (their sums are no longer read).
+// The result goes to nrep rows of w, ne0 apart (matrices that share U).
+DEV double readlane_f64(double v, int lane) {
+    const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)b, lane);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(b >> 32), lane);
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
+__global__ __launch_bounds__(64) void k_schur_weights(const double *__restrict__ U, int64_t ne0, float *__restrict__ w,
+                                                      int64_t nrep) {
+    const int64_t c0 = (int64_t)blockIdx.y * QK;
+    const int i = (int)blockIdx.x, lane = lane_id();
+    const double *ub = U + c0 * ne0 + c0;          // U_BB[s][t] = ub[s * ne0 + t]
+    double acc[4] = {0.0, 0.0, 0.0, 0.0}, u[4], un[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) u[q] = ub[(int64_t)i * ne0 + 64 * q + lane];
+    double ws = 0.0;
+    for (int t = i; t < QK; ++t) {
+        const int tn = t + 1 < QK ? t + 1 : t;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) un[q] = ub[(int64_t)tn * ne0 + 64 * q + lane];
+        const int qt = t >> 6, lt = t & 63;        // column t: lane lt, slot qt
+        const double at = readlane_f64(qt == 0 ? acc[0] : qt == 1 ? acc[1] : qt == 2 ? acc[2] : acc[3], lt);
+        const double dt = readlane_f64(qt == 0 ? u[0] : qt == 1 ? u[1] : qt == 2 ? u[2] : u[3], lt);
+        const double x = ((t == i ? 1.0 : 0.0) - at) / dt;
+        ws = fma(x, x, ws);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            acc[q] = fma(x, u[q], acc[q]);
+            u[q] = un[q];
+        }
+    }
+    if (lane == 0)
+        for (int64_t r = 0; r < nrep; ++r) w[r * ne0 + c0 + i] = (float)ws;
+}

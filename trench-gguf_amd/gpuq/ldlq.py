@@ -111,6 +111,21 @@ def block_weights(mode, U=None, perm=None, diag_n=None, imatrix=None, bs=QK_K):
     raise ValueError(mode)
 
 
+def schur_weights_dev(gq, U, nrep=1, stream=None):
+    """the 'schur' importance of every block of a device factor U (torch f64 [ne0, ne0]) on the device, in the
+    library's fixed order (gpuq_schur_weights_dev): torch f32 [nrep, ne0], one row a matrix that shares U"""
+    import torch
+    U = U.to(torch.float64).contiguous()
+    ne0 = U.shape[0]
+    w = torch.empty((nrep, ne0), dtype=torch.float32, device=U.device)
+    if stream is None:
+        stream = torch.cuda.current_stream().cuda_stream
+    rc = gq.gpuq_schur_weights_dev(U.data_ptr(), ne0, w.data_ptr(), nrep, stream)
+    if rc != 0:
+        raise RuntimeError("gpuq_schur_weights_dev failed (%d)" % rc)
+    return w
+
+
 def proxy_loss(W, deq, H, n):
     """tr((W - Q) H (W - Q)^T) / n, the calibration inputs' squared output error that the feedback lowers
     (tools/ldlq.py:110-113): W and deq [ne1, ne0] in the original column order, H [ne0, ne0]"""
@@ -140,24 +155,31 @@ def quantize_matrix_dev(gq, typ, W, U, perm, qw, feedback=True, u_per_matrix=Fal
     return out
 
 
-def quantize_matrix_host(gq, typ, W, H, n, imatrix=None, damp=0.01, order="seq", h_per_matrix=False):
+WEIGHTS = {"imatrix": 0, "diag": 1, "schur": 2}
+
+
+def quantize_matrix_host(gq, typ, W, H, n, imatrix=None, damp=0.01, order="seq", h_per_matrix=False,
+                         weights="imatrix"):
     """The whole LDLQ path from numpy, no framework: W f32 [B, ne1, ne0] (original column order), H f64 [ne0, ne0]
     (or [B, ne0, ne0] with h_per_matrix) the Hessian sum over n inputs, imatrix f32 [B, ne0] (or [ne0] for all).
-    The factor is built on the device (gpuq_prepare_hessian_dev) and the loop runs there (gpuq_ldlq_dev), weights =
-    the imatrix in the permuted order as tools/ldlq.py's default. Returns uint8 [B, ne1, nblk * block_bytes]."""
+    The factor is built on the device (gpuq_prepare_hessian_dev) and the loop runs there (gpuq_ldlq_dev). weights as
+    tools/ldlq.py's: 'imatrix' (the imatrix in the permuted order), 'diag' (diag(H)/n) or 'schur' (diag((U_BB^T
+    U_BB)^-1) of each block); imatrix is not used for the last two. Returns uint8 [B, ne1, nblk * block_bytes]."""
+    if weights not in WEIGHTS:
+        raise ValueError(weights)
     W = np.ascontiguousarray(W, dtype=np.float32)
     if W.ndim == 2:
         W = W[None]
     B, ne1, ne0 = W.shape
     H = np.ascontiguousarray(H, dtype=np.float64)
     im = None
-    if imatrix is not None:
+    if imatrix is not None and weights == "imatrix":
         im = np.ascontiguousarray(np.broadcast_to(np.asarray(imatrix, dtype=np.float32), (B, ne0)))
     tsize = gq.gpuq_block_bytes(int(typ))
     out = np.empty((B, ne1, ne0 // QK_K * tsize), dtype=np.uint8)
     got = gq.gpuq_ldlq(int(typ), W.ctypes.data, H.ctypes.data, ne0 * ne0 if h_per_matrix else 0, float(n), float(damp),
-                       1 if order == "act" else 0, None if im is None else im.ctypes.data, B, ne1, ne0,
-                       out.ctypes.data)
+                       1 if order == "act" else 0, WEIGHTS[weights], None if im is None else im.ctypes.data, B, ne1,
+                       ne0, out.ctypes.data)
     if got != out.nbytes:
         raise RuntimeError("gpuq_ldlq failed (type %d, %d x %d x %d)" % (int(typ), B, ne1, ne0))
     return out

@@ -1,7 +1,8 @@
 """Re-quantize the tensors of a (split) GGUF that a rules file names, on the MI355X, and copy the rest byte for byte.
 
     python requant.py <in shard 1> <out dir> <rules file> [--imatrix=<imatrix.gguf>] [--check] [--gpu=N]
-                      [--only-matched] [--hessian=<dir> [--damp=0.01] [--damp-iq1=D] [--order=seq|act] [--gated]]
+                      [--only-matched] [--hessian=<dir> [--damp=0.01] [--damp-iq1=D] [--order=seq|act] [--gated]
+                      [--weights=imatrix|diag|schur]] [--allow-synthetic-tables]
 
 This is the plan-and-write part of the reference's tools/requant_experts.py (rules: 171-177; fallback types:
 180-192; imatrix normalization: 280-293; the per-shard plan: 420-470; the writer: 471-500) with its quantizer
@@ -14,13 +15,18 @@ whose regex matches anywhere in the name wins.
 reference's driver does (tools/requant_experts.py:200-212, 520-600): blk.L.in.npy [n_expert, ne0, ne0] for
 ffn_gate/up_exps, blk.L.mid.npy for ffn_down_exps (blk.L.in_g / mid_g with --gated), blk.L.counts.npy the rows
 each expert's Hessian summed. Each expert runs libgpuq's whole LDLQ path (gpuq_ldlq: the factor and the loop on the
-device, the imatrix row as the importance); an expert with fewer than LDLQ_MIN_ROWS (64) rows is rounded plain.
-Sources for it: F32, F16 and BF16 (widened to f32 exactly on the host).
+device); the importance a super-block's quantizer gets is --weights (the imatrix row by default, 'diag' for diag(H)/n
+or 'schur'); a tensor without imatrix data, and an expert with fewer than LDLQ_MIN_ROWS (64) rows, are rounded plain
+(tools/requant_experts.py:551-552). Sources for it: F32, F16 and BF16 (widened to f32 exactly on the host).
 
-Not here (the reference's other paths): --dump / --dense-dump Hessians, --weights other than imatrix, --sub, the
-CPU quantizer, sources in other stored types and the fallback types that libgpuq does not produce (Q4_0, Q5_0,
-Q5_1, F16). A tensor that needs one of these stops the run with its name and the reason; nothing falls back to the
-CPU.
+--allow-synthetic-tables: the package's own gpuq_tables.bin holds stand-in IQ1/IQ2/IQ3 codebooks (ggml's are not
+part of this repository) and carries a mark that makes libgpuq refuse those types, because llama.cpp would read the
+grid indices against ggml's own grids. This flag lifts that refusal for test runs. A gpuq_tables.bin written from
+ggml by the reference's gpuq_tables.c needs no flag.
+
+Not here (the reference's other paths): --dump / --dense-dump Hessians, --sub, the CPU quantizer, sources in other
+stored types and the fallback types that libgpuq does not produce (Q4_0, Q5_0, Q5_1, F16). A tensor that needs one
+of these stops the run with its name and the reason; nothing falls back to the CPU.
 """
 import os
 import re
@@ -32,7 +38,7 @@ import numpy as np
 if __package__ in (None, ""):
     sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
 import gpuq  # noqa: E402
-from gpuq import gguf_io  # noqa: E402
+from gpuq import gguf_io, tables  # noqa: E402
 
 T = gguf_io.TYPE_BY_NAME
 # llama-quantize's tensor_type_fallback for rows that are not whole blocks of the asked type
@@ -129,11 +135,15 @@ class Step:
         self.hessian = hessian          # (Hessian .npy, counts .npy) for error-feedback rounding, or None
 
 
-def plan_shard(reader, rules, imat, can_quantize=None, hess=None):
+TABLE_TYPES = {T["IQ1_S"], T["IQ1_M"], T["IQ2_XXS"], T["IQ2_XS"], T["IQ2_S"], T["IQ3_XXS"], T["IQ3_S"]}
+
+
+def plan_shard(reader, rules, imat, can_quantize=None, hess=None, can_ldlq=None):
     """the plan of one shard (tools/requant_experts.py:420-470): the rule's type, fitted to the row length; an
     i-quant that needs an imatrix the file does not hold, or one of the wrong shape, leaves the tensor as it is; a
     type that takes one quantizes without it then. can_quantize(type, with_imatrix) -> bool is libgpuq's
-    gpuq_can_quantize (None: plan only). hess: {"dir", "gated"} for error-feedback rounding, or None."""
+    gpuq_can_quantize (None: plan only). hess: {"dir", "gated"} for error-feedback rounding, or None; can_ldlq(type)
+    -> bool is libgpuq's gpuq_can_dequantize_type (the loop reads each block back; None: plan only)."""
     plan = []
     for t in reader.tensors:
         typ = rule_type(rules, t.name)
@@ -164,8 +174,12 @@ def plan_shard(reader, rules, imat, can_quantize=None, hess=None):
             plan.append(Step(t, note=note))
             continue
         if typ not in gpuq.TYPE_NAMES or (can_quantize is not None and not can_quantize(typ, im is not None)):
-            raise RequantError("%s: libgpuq does not quantize %s%s" % (
-                t.name, gguf_io.type_name(typ), "" if im is not None else " without an imatrix"))
+            why = ""
+            if typ in TABLE_TYPES and os.path.exists(gpuq.tables_path()) and tables.is_synthetic(gpuq.tables_path()):
+                why = (" (%s holds the package's stand-in codebooks, refused outside tests: use a table file written "
+                       "from ggml, or --allow-synthetic-tables for a test run)" % gpuq.tables_path())
+            raise RequantError("%s: libgpuq does not quantize %s%s%s" % (
+                t.name, gguf_io.type_name(typ), "" if im is not None else " without an imatrix", why))
         if t.tensor_type not in SOURCES:
             raise RequantError("%s: stored as %s, which libgpuq does not decode (F32, F16, BF16, Q8_0, MXFP4)" % (
                 t.name, gguf_io.type_name(t.tensor_type)))
@@ -179,6 +193,8 @@ def plan_shard(reader, rules, imat, can_quantize=None, hess=None):
                        "no imatrix" if im is None else
                        "%s is not rounded per 256-weight super-block" % gguf_io.type_name(typ)
                        if typ not in LDLQ_TYPES or t.shape[0] % 256 else
+                       "libgpuq cannot read %s back" % gguf_io.type_name(typ)
+                       if can_ldlq is not None and not can_ldlq(typ) else
                        "stored as %s (error feedback reads F32 / F16 / BF16)" % gguf_io.type_name(t.tensor_type)
                        if t.tensor_type not in (gpuq.F32, gpuq.F16, gpuq.BF16) else None)
                 if why is not None:
@@ -217,8 +233,8 @@ def quantize_tensor(gq, step, batch_floats, hess=None):
 
 def quantize_tensor_ldlq(gq, step, hess, out):
     """error-feedback rounding, expert by expert: the expert's Hessian and row count from the folder, the whole LDLQ
-    path on the device (gpuq_ldlq), the expert's imatrix row as the importance; plain rounding for an expert with
-    fewer than MIN_ROWS rows"""
+    path on the device (gpuq_ldlq), the importance hess["weights"] (the expert's imatrix row by default); plain
+    rounding for an expert with fewer than MIN_ROWS rows"""
     from gpuq import ldlq
     t = step.tensor
     ne0, ne1, ne2 = t.shape
@@ -228,6 +244,7 @@ def quantize_tensor_ldlq(gq, step, hess, out):
         damp = hess["damp_iq1"]
     H_all = np.load(step.hessian[0], mmap_mode="r")
     counts = np.asarray(np.load(step.hessian[1])).reshape(-1)
+    weights = hess.get("weights", "imatrix")
     per = t.n_bytes // ne2
     dst = out.reshape(ne2, -1)
     for e in range(ne2):
@@ -240,8 +257,11 @@ def quantize_tensor_ldlq(gq, step, hess, out):
                 raise RequantError("%s: gpuq_quantize failed for expert %d" % (t.name, e))
             continue
         H = np.asarray(H_all[e], dtype=np.float64)
-        dst[e] = ldlq.quantize_matrix_host(gq, typ, w, H, n, im, damp=damp,
-                                           order=hess.get("order", "seq")).reshape(-1)
+        try:
+            dst[e] = ldlq.quantize_matrix_host(gq, typ, w, H, n, im, damp=damp, order=hess.get("order", "seq"),
+                                               weights=weights).reshape(-1)
+        except RuntimeError as err:
+            raise RequantError("%s, expert %d: %s" % (t.name, e, err)) from err
     return out
 
 
@@ -277,6 +297,7 @@ def run(shard1, out_dir, rules_path, imatrix_path=None, check=False, device=0, o
     if gq is None and not check:
         gq = gpuq.load_gpuq(device)
     can = None if gq is None else (lambda typ, with_im: gq.gpuq_can_quantize(typ, 1 if with_im else 0) == 1)
+    can_ldlq = None if gq is None else (lambda typ: gq.gpuq_can_dequantize_type(typ) == 1)
     batch_floats = int(os.environ.get("GPUQ_BATCH_MB", "2048")) << 20
     paths = shard_paths(shard1)
     if not check:
@@ -290,7 +311,7 @@ def run(shard1, out_dir, rules_path, imatrix_path=None, check=False, device=0, o
         r = first if sh == paths[0] else gguf_io.GGUFReader(sh)
         out = os.path.join(out_dir, os.path.basename(sh))
         log("%s -> %s" % (sh, out))
-        plan = plan_shard(r, rules, imat, can, hess)
+        plan = plan_shard(r, rules, imat, can, hess, can_ldlq)
         for s in plan:
             if s.note:
                 log("  %s: %s" % (s.tensor.name, s.note))
@@ -315,7 +336,7 @@ def main(argv=None):
     flags = [a for a in argv if a.startswith("--")]
     args = [a for a in argv if not a.startswith("--")]
     known = ("--imatrix=", "--gpu=", "--check", "--only-matched", "--hessian=", "--damp=", "--damp-iq1=",
-             "--order=", "--gated")
+             "--order=", "--gated", "--weights=", "--allow-synthetic-tables")
     bad = [f for f in flags if not f.startswith(known)]
     if len(args) != 3 or bad:
         print(__doc__.split("\n\n")[1], file=sys.stderr)
@@ -329,13 +350,18 @@ def main(argv=None):
     if "--hessian" in opt:
         hess = {"dir": opt["--hessian"], "damp": float(opt.get("--damp", 0.01)), "gated": "--gated" in flags,
                 "damp_iq1": float(opt["--damp-iq1"]) if "--damp-iq1" in opt else None,
-                "order": opt.get("--order", "seq")}
+                "order": opt.get("--order", "seq"), "weights": opt.get("--weights", "imatrix")}
         if hess["order"] not in ("seq", "act"):
             print("--order is seq or act", file=sys.stderr)
             return 2
+        if hess["weights"] not in ("imatrix", "diag", "schur"):
+            print("--weights is imatrix, diag or schur", file=sys.stderr)
+            return 2
+    if "--allow-synthetic-tables" in flags:
+        os.environ["GPUQ_ALLOW_SYNTHETIC_TABLES"] = "1"
     try:
         run(args[0], args[1], args[2], imat, "--check" in flags, dev, "--only-matched" in flags, hess=hess)
-    except RequantError as e:
+    except (RequantError, RuntimeError, OSError) as e:
         print("error: %s" % e, file=sys.stderr)
         return 1
     return 0

@@ -19,7 +19,13 @@ same tables:
   - dequantizer grids: IQ2 levels -> {8, 25, 43, 59}, IQ3_XXS levels -> {4, 12, 20, 28, 36, 44, 52, 62}, IQ3_S
     levels -> {1, 3, ..., 15}, IQ1 levels -> {-1, 0, 1}: what each to_float's scale arithmetic expects.
 A gpuq_tables.bin written by the reference's gpuq_tables.c from ggml's own code replaces this file one for one.
+
+The file written here ends with one more record, the stand-in mark: type 0x53594e54 with one grid entry (the bytes
+"SYNTHTAB") and no map or neighbours. The reference's loader keeps it as a table of a type nothing asks for; libgpuq's
+gpuq_init loads the stand-in IQ1/IQ2/IQ3 tables of a marked file only when GPUQ_ALLOW_SYNTHETIC_TABLES=1 is set
+(tests and benchmarks), so that no model file is written with grid indices into stand-in codebooks by accident.
 """
+import hashlib
 import struct
 
 import numpy as np
@@ -27,6 +33,8 @@ import numpy as np
 IQ2_XXS, IQ2_XS, IQ3_XXS, IQ1_S, IQ3_S, IQ2_S = 16, 17, 18, 19, 21, 22
 MAP2 = 43692    # 2-bit keys of 8 levels up to the all-2 key 0xAAAA (+ slack), ggml's kmap_size
 MAP3 = 4096     # 3-bit keys of 4 levels
+MARK = 0x53594E54                                   # the stand-in mark's record type
+MARK_GRID = np.frombuffer(b"SYNTHTAB", dtype="<u8")  # its one grid entry
 
 # (type, grid points, levels a coordinate, values a point, neighbour distance shells)
 SPECS = [
@@ -130,8 +138,15 @@ def synthetic_tables():
     return recs
 
 
-def write_tables(path, recs=None):
-    recs = synthetic_tables() if recs is None else recs
+def mark_record():
+    return (MARK, MARK_GRID.copy(), np.zeros(0, dtype=np.int32), np.zeros(0, dtype=np.uint16))
+
+
+def write_tables(path, recs=None, mark=True):
+    """recs (default: the stand-ins) in the file layout, followed by the stand-in mark unless mark=False"""
+    recs = list(synthetic_tables() if recs is None else recs)
+    if mark:
+        recs.append(mark_record())
     with open(path, "wb") as f:
         for typ, grid, kmap, neigh in recs:
             f.write(struct.pack("<4i", typ, len(grid), len(kmap), len(neigh)))
@@ -155,6 +170,21 @@ def read_tables(path):
         neigh = np.frombuffer(data, dtype="<u2", count=n, offset=o); o += 2 * n
         out[typ] = (grid, kmap, neigh)
     return out
+
+
+def is_synthetic(path):
+    """the file carries the stand-in mark"""
+    return MARK in read_tables(path)
+
+
+def content_sha(path):
+    """sha256 of the table records without the stand-in mark (the mark is written last, so this is the hash of the
+    file as it was before the mark existed)"""
+    data = open(path, "rb").read()
+    tail = 16 + 8
+    if len(data) >= tail and struct.unpack_from("<4i", data, len(data) - tail) == (MARK, 1, 0, 0):
+        data = data[:-tail]
+    return hashlib.sha256(data).hexdigest()
 
 
 if __name__ == "__main__":
