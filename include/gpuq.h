@@ -95,6 +95,16 @@ size_t gpuq_requantize_dev(int src_type, const void *d_raw, int type, void *d_ds
 size_t gpuq_ldlq_dev(int type, float *d_wp, const double *d_u, int64_t u_stride, const float *d_qw, int64_t nmat,
                      int64_t ne1, int64_t ne0, const int64_t *blk_order, int feedback, void *d_out, void *stream);
 
+/* gpuq_ldlq_dev that allocates nothing. No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments,
+ * checks and bytes as gpuq_ldlq_dev; its Es scratch is a static 32 MiB device array of the library (each GPU it runs
+ * on holds one until the process ends), every launch goes to `stream`, and it calls no allocator. Limit: with
+ * feedback, nmat * ne1 <= 8192 rows; a larger call returns 0 (with a message on stderr) before any launch. Calls on
+ * one GPU share the array: calls that overlap on one GPU race. */
+size_t gpuq_ldlq_dev_noalloc(int type, float *d_wp, const double *d_u, int64_t u_stride, const float *d_qw,
+                             int64_t nmat, int64_t ne1, int64_t ne0, const int64_t *blk_order, int feedback,
+                             void *d_out, void *stream);
+
 /* H += X^T X on the device, replacing the float32-GEMM / float64-sum loop of tools/hessian_from_dump.py:73-79:
  * d_X [nrows][ne0] f32, d_H [ne0][ne0] f64 (symmetric, kept symmetric), products exact in f64, sums over the rows in
  * order on the f64 matrix cores. Asynchronous on `stream`. Returns 0; 1 bad arguments (ne0 a multiple of 256, at

@@ -29,7 +29,16 @@
 
 extern "C" size_t gpuq_block_bytes(int type);
 
+// The Es scratch of gpuq_ldlq_dev_noalloc, the entry point that allocates nothing: two blocks of Es (2 x 256 doubles
+// a row) for up to LDLQ_SCRATCH_ROWS rows (nmat * ne1), 32 MiB, held by every device the library runs on for the
+// life of the process. Host code never passes this name to a kernel or a copy (on the host it is only a stand-in):
+// gpuq_init takes each device's address of it with hipGetSymbolAddress, once per device, into g_scratch.
+static constexpr int64_t LDLQ_SCRATCH_ROWS = 8192;
+static __device__ __align__(256) double scratch[2 * LDLQ_SCRATCH_ROWS * 256];
+
 namespace {
+
+double *g_scratch[64] = {};    // per device: the device address of `scratch`
 
 struct Tabs {
     bool ok = false;
@@ -507,6 +516,11 @@ bool launch_solve(int type, const float *W, const uint8_t *q, int64_t q_stride, 
 extern "C" int gpuq_init(const char *tables, int device) {
     std::lock_guard<std::mutex> lock(g_mu);
     if (hipSetDevice(device) != hipSuccess) return 1;
+    if (device >= 0 && device < 64 && !g_scratch[device]) {     // (the device is current)
+        void *ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return 4;
+        g_scratch[device] = (double *)ptr;
+    }
     int ncu = 0;
     if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && ncu > 0) g_ncu = ncu;
     if (!g_err && hipMalloc((void **)&g_err, sizeof(int)) != hipSuccess) return 4;
@@ -812,6 +826,29 @@ extern "C" size_t gpuq_ldlq_dev(int type, float *d_wp, const double *d_u, int64_
         if (hipEventRecord(g_ev_done, st) != hipSuccess) return 0;
         g_ldlq_pending = true;
     }
+    return (size_t)(rows * nblk * bb);
+}
+
+// gpuq_ldlq_dev for callers that cannot allocate (code under HIP graph capture, serving loops): the same loop with
+// the same bytes, its Es in the library's static `scratch` array instead of a buffer it grows, every launch on
+// `stream` (no side stream), no event, lock or allocation. At most LDLQ_SCRATCH_ROWS rows (nmat * ne1) with feedback;
+// a larger call is refused before any launch. Calls share the device's array: calls that overlap on one GPU race.
+extern "C" size_t gpuq_ldlq_dev_noalloc(int type, float *d_wp, const double *d_u, int64_t u_stride, const float *d_qw,
+                                        int64_t nmat, int64_t ne1, int64_t ne0, const int64_t *blk_order,
+                                        int feedback, void *d_out, void *stream) {
+    if (!ldlq_args_ok(type, d_wp, d_u, u_stride, d_qw, nmat, ne1, ne0, blk_order, d_out)) return 0;
+    const int64_t nblk = ne0 / QK, bb = (int64_t)gpuq_block_bytes(type), rows = nmat * ne1;
+    const bool fb = feedback && nblk > 1;
+    double *es = g_device >= 0 && g_device < 64 ? g_scratch[g_device] : nullptr;
+    if (fb && !es) return 0;
+    if (fb && rows > LDLQ_SCRATCH_ROWS) {
+        fprintf(stderr, "gpuq_ldlq_dev_noalloc: %lld rows (nmat x ne1) exceed the scratch maximum of %lld\n",
+                (long long)rows, (long long)LDLQ_SCRATCH_ROWS);
+        return 0;
+    }
+    if (!ldlq_loop(type, d_wp, d_u, u_stride, d_qw, nmat, ne1, ne0, blk_order, fb, d_out, (hipStream_t)stream, es,
+                   false))
+        return 0;
     return (size_t)(rows * nblk * bb);
 }
 

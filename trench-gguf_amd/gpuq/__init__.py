@@ -38,6 +38,7 @@ SIGNATURES = {
     "gpuq_requantize_dev": (_sz, [_i, _vp, _i, _vp, _i64, _i64, _i64, _vp, _vp]),
     "gpuq_take_error": (_i, []),
     "gpuq_ldlq_dev": (_sz, [_i, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp, _i, _vp, _vp]),
+    "gpuq_ldlq_dev_noalloc": (_sz, [_i, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp, _i, _vp, _vp]),
     "gpuq_hessian_accumulate_dev": (_i, [_vp, _i64, _i64, _vp, _vp]),
     "gpuq_prepare_hessian_dev": (_i, [_vp, _i64, ctypes.c_double, ctypes.c_double, _i, _vp, _vp, _vp, _vp, _vp]),
     "gpuq_schur_weights_dev": (_i, [_vp, _i64, _vp, _i64, _vp]),
