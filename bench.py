@@ -1,21 +1,29 @@
 #!/usr/bin/env python3
 """bench.py - throughput of the MI355X GGUF quantizer on the configured synthetic workloads.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-host] [--quick]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-host] [--only NAME,...] [--experts N]
 
 One "step" is one pass of the quantizer over one workload tensor already resident in HBM (the device entry point
-gpuq_requantize_dev: source bytes decoded in registers, quantized, blocks written to HBM). The headline line is the
-Q4_K-with-imatrix workload on a 2048 x 7168 BF16 tensor (N(0, 0.02) plus 0.1% outliers at +-8 sigma, a log-normal
-imatrix); `per_type` adds Q6_K on the same tensor, Q8_0 on a 4096 x 4096 F32 tensor, IQ2_XXS on 256 x 2048 x 7168
-BF16 experts and IQ1_S / IQ1_M on 384 x 2048 x 7168 MXFP4 experts; `other_types` the remaining nine types on the
-headline tensor (GPU rate, roofline, byte spot check on 64 rows). Kernel time comes from HIP events on the launch
-stream; inputs that fit the 256 MB Infinity Cache are rotated over enough copies that every launch reads HBM.
+gpuq_requantize_dev: source bytes decoded in registers, quantized, blocks written to HBM). The headline line is
+IQ2_XXS with imatrix on 256 stacked BF16 experts of 2048 x 7168 (expert e ~ N(0, s_e), s_e ~ U[0.01, 0.03], a
+log-normal(0, 1.5) imatrix a expert). `per_type` adds Q8_0 on a 4096 x 4096 F32 tensor, Q4_K and Q6_K on a
+2048 x 7168 BF16 tensor (N(0, 0.02) plus 0.1% outliers at +-8 sigma, a log-normal imatrix), IQ1_S / IQ1_M on 384 x
+2048 x 7168 MXFP4 experts and IQ2_S with LDLQ error feedback on 64 BF16 experts; `other_types` the remaining nine
+types on the 2048 x 7168 tensor (GPU rate, roofline, byte spot check on 64 rows). Kernel time comes from HIP events
+on the launch stream; inputs that fit the 256 MB Infinity Cache are rotated over enough copies that every launch
+reads HBM.
 
-Each entry carries a roofline (HBM bytes for Q8_0, VALU operations for the searches: the sequential algorithm's
-fp32/int operation count per weight, measured by the op-counting build of the CPU oracle on a sample of the same
-tensor) and the CPU baseline: the oracle (a C restatement of ggml_quantize_chunk, -O2 without FMA) on all the host
-cores this process may use, timed on a bounded sample of the same tensor, whose bytes are also compared with the
-GPU's as a spot check.
+Each entry carries a roofline and a CPU baseline:
+- roofline: HBM bytes for Q8_0 against 8 TB/s; for the searches, the sequential algorithm's VALU operations (each
+  add, mul, compare, select, convert one; the oracle's op-counting build run on a sample of the same tensor) against
+  78.6 T operations/s, MI355X's published FP32 vector peak of 157.3 TFLOP/s counted per instruction (an FMA is two
+  flops): two wave64 VALU instructions per SIMD per four clocks, 1,024 SIMDs, 2.4 GHz. `traffic` (HBM bytes a launch)
+  and `valu_issue` (instructions issued per SIMD per clock, rocprof's VALUBusy) come from the committed rocprofv3
+  counter summaries under profiles/;
+- cpu_baseline: the oracle (a C restatement of ggml_quantize_chunk, -O2 without FMA) on all the host cores this
+  process may use, timed on a bounded sample of the same tensor whose bytes are also compared with the GPU's; for
+  LDLQ the reference's CPU loop order (numpy LU solve and BLAS product a block, tools/ldlq.py:103-106, one expert a
+  thread) around the oracle's quantizer.
 """
 import argparse
 import json
@@ -31,29 +39,46 @@ sys.path.insert(0, os.path.join(ROOT, "oracle"))
 
 METRIC = "Mweights/s per type (Q8_0, Q4_K, IQ2_XXS, IQ1_M) on 1 MI355X; % VALU/HBM peak"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
-VALU_PEAK_TOPS = 39.3          # 256 CUs x 64 lanes x 2.4 GHz, non-packed fp32/int lane-operations, T/s
+VALU_PEAK_TOPS = 78.6          # 157.3 TFLOP/s FP32 vector / 2 flops an FMA: 2 wave64 instr / SIMD / 4 clk, 2.4 GHz
+FP64_PEAK_TFLOPS = 78.6        # MI355X FP64 (vector and matrix)
 MALL_BYTES = 256 << 20         # Infinity Cache
 CPU_MIN_S = 10.0               # the CPU baseline repeats its sample until this much CPU time has run
+ENTRIES = ["IQ2_XXS", "Q8_0", "Q4_K", "Q6_K", "IQ1_S", "IQ1_M", "LDLQ", "other"]
+OTHER = ["Q2_K", "Q3_K", "Q5_K", "IQ4_NL", "IQ4_XS", "IQ2_XS", "IQ2_S", "IQ3_XXS", "IQ3_S"]
 
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def pmc_traffic(key):
-    """HBM bytes per launch of a kernel as measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on this workload and
-    scaled by the same counters' reading for a copy kernel of known size (profiles/hbm_traffic_pmc.md; the lines
-    `traffic[<key>] = <bytes>`), or None when not measured on this workload"""
-    path = os.path.join(ROOT, "profiles", "hbm_traffic_pmc.md")
+def profile_value(fname, tag, key):
+    """the value of a line `<tag>[<key>] = <value>` in profiles/<fname> (a committed rocprofv3 summary), or None"""
     try:
-        with open(path) as f:
+        with open(os.path.join(ROOT, "profiles", fname)) as f:
             for line in f:
                 line = line.strip().strip("`")
-                if line.startswith("traffic[%s] = " % key):
-                    return int(line.split("=", 1)[1])
+                if line.startswith("%s[%s] = " % (tag, key)):
+                    return line.split("=", 1)[1].strip()
     except OSError:
         pass
     return None
+
+
+def pmc_traffic(key):
+    """HBM bytes a launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on this workload, scaled by the same counters'
+    reading for a copy kernel of known size (profiles/hbm_traffic_pmc.md), or None when not measured"""
+    v = profile_value("hbm_traffic_pmc.md", "traffic", key)
+    return None if v is None else int(v)
+
+
+def pmc_valu(key):
+    """{issue_per_simd_clk, valu_busy_pct, lane_util} from profiles/valu_counters_pmc.md, or None"""
+    v = profile_value("valu_counters_pmc.md", "valu", key)
+    if v is None:
+        return None
+    issue, busy, util = v.split()
+    return {"issue_per_simd_clk": float(issue), "valu_busy_pct": float(busy), "lane_util": float(util),
+            "source": "profiles/valu_counters_pmc.md"}
 
 
 def cpu_threads():
@@ -63,11 +88,22 @@ def cpu_threads():
         return os.cpu_count() or 1
 
 
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 class Workload:
     """a synthetic tensor in HBM (source bytes, imatrix) plus its host-side sample for the CPU leg"""
 
-    def __init__(self, name, src, nmat, nrow, ncol, raw, imatrix):
-        self.name, self.src, self.nmat, self.nrow, self.ncol = name, src, nmat, nrow, ncol
+    def __init__(self, name, key, src, nmat, nrow, ncol, raw, imatrix):
+        self.name, self.key, self.src, self.nmat, self.nrow, self.ncol = name, key, src, nmat, nrow, ncol
         self.raw, self.imatrix = raw, imatrix
         self.n = nmat * nrow * ncol
 
@@ -79,7 +115,7 @@ def make_f32(torch, gen, shape, sigma):
 def wl_c1(torch, gpuq):
     g = torch.Generator(device="cuda").manual_seed(0)
     x = make_f32(torch, g, (4096, 4096), 0.02)
-    return Workload("F32 4096x4096 N(0,0.02), seed 0", gpuq.F32, 1, 4096, 4096, x, None)
+    return Workload("F32 4096x4096 N(0,0.02), seed 0", "F32 4096x4096", gpuq.F32, 1, 4096, 4096, x, None)
 
 
 def wl_c2(torch, gpuq):
@@ -92,7 +128,7 @@ def wl_c2(torch, gpuq):
     raw = x.to(torch.bfloat16).contiguous()                       # RNE to BF16
     im = torch.exp(torch.randn(1, 7168, device="cuda", generator=g) * 1.5).contiguous()
     return Workload("BF16 2048x7168 N(0,0.02) + 0.1% outliers at +-8 sigma, log-normal(0,1.5) imatrix",
-                    gpuq.BF16, 1, 2048, 7168, raw, im)
+                    "BF16 2048x7168", gpuq.BF16, 1, 2048, 7168, raw, im)
 
 
 def wl_c3(torch, gpuq, nexp=256):
@@ -104,7 +140,7 @@ def wl_c3(torch, gpuq, nexp=256):
                          * sig[e:e + 16]).to(torch.bfloat16)
     im = torch.exp(torch.randn(nexp, 7168, device="cuda", generator=g) * 1.5).contiguous()
     return Workload("BF16 %dx2048x7168 experts, N(0, s_e), s_e ~ U[0.01,0.03], per-expert log-normal(0,1.5) imatrix"
-                    % nexp, gpuq.BF16, nexp, 2048, 7168, raw.reshape(-1), im)
+                    % nexp, "BF16 %dx2048x7168" % nexp, gpuq.BF16, nexp, 2048, 7168, raw.reshape(-1), im)
 
 
 def wl_c4(torch, gpuq, nexp=384):
@@ -114,7 +150,8 @@ def wl_c4(torch, gpuq, nexp=384):
     raw[:, 0] = (127 + torch.randint(-8, -3, (nblk,), device="cuda", generator=g)).to(torch.uint8)
     im = torch.exp(torch.randn(nexp, 7168, device="cuda", generator=g) * 1.5).contiguous()
     return Workload("MXFP4 %dx2048x7168 experts, e8m0 exponents U{-8..-4}, uniform e2m1 codes, per-expert "
-                    "log-normal(0,1.5) imatrix" % nexp, gpuq.MXFP4, nexp, 2048, 7168, raw.reshape(-1), im)
+                    "log-normal(0,1.5) imatrix" % nexp, "MXFP4 %dx2048x7168" % nexp, gpuq.MXFP4, nexp, 2048, 7168,
+                    raw.reshape(-1), im)
 
 
 def wl_c5(torch, gpuq, ldlq, nexp=64, ncal=8192):
@@ -139,9 +176,28 @@ def wl_c5(torch, gpuq, ldlq, nexp=64, ncal=8192):
     return W, Us, perm, im
 
 
+def blas_ldlq_rows(orc, typ, Wp, U, qw):
+    """the reference's CPU loop (tools/ldlq.py:71-107) in numpy's order on permuted rows Wp [rows, ne0]: the oracle
+    quantizes and reads back each block, np.linalg.solve gives E U_BB^-1, a BLAS product the update. Returns the
+    bytes of each permuted block"""
+    Wp = Wp.copy()
+    rows, ne0 = Wp.shape
+    nblk = ne0 // 256
+    out = []
+    for k in range(nblk):
+        cols = slice(256 * k, 256 * (k + 1))
+        blk = np.ascontiguousarray(Wp[:, cols])
+        raw = orc.quantize(typ, blk, qw[cols])
+        out.append(raw)
+        if k + 1 < nblk:
+            q = orc.dequantize(typ, raw, rows * 256).reshape(rows, 256)
+            Es = np.linalg.solve(U[cols, cols].T, (blk - q).T).T
+            Wp[:, 256 * (k + 1):] -= (Es @ U[cols, 256 * (k + 1):]).astype(np.float32)
+    return out
+
+
 def bench_ldlq(torch, gq, gpuq, orc, steps, want_cpu, nexp):
     """IQ2_S with LDLQ error feedback over 64 experts; one step = the whole loop (gpuq_ldlq_dev)"""
-    import numpy as np
     from gpuq import ldlq
     t0 = time.time()
     W, Us, perm, im = wl_c5(torch, gpuq, ldlq, nexp)
@@ -176,29 +232,47 @@ def bench_ldlq(torch, gq, gpuq, orc, steps, want_cpu, nexp):
                      "per-expert H from 8192 Student-t(4) activations" % nexp_,
          "value": round(n / (ms / 1e3) / 1e6, 1), "unit": "Mweights/s", "ms_per_step": round(ms, 2),
          "steps": steps,
-         "roofline": {"bound": "fp64", "achieved": round(flops / (ms / 1e3) / 1e12, 2), "peak": 78.6,
-                      "unit": "TFLOP/s", "frac": round(flops / (ms / 1e3) / 1e12 / 78.6, 4), "traffic": None,
-                      "algorithmic_flops_per_step": flops, "note": "whole loop time (quantize + solve + update)"}}
-    # CPU leg and spot check: rows are independent in the loop, so a row sample of expert 0 is exact (the whole
-    # expert when the CPU is timed, a few rows for the check alone)
-    rows = ne1 if want_cpu else 16 * max(1, cpu_threads() // 4)
-    U0 = Us[0].cpu().numpy()
-    Wp_s = Wp0[0:1, :rows].cpu().numpy()
-    qw0 = qw[0:1].cpu().numpy()
+         "roofline": {"bound": "fp64", "achieved": round(flops / (ms / 1e3) / 1e12, 2), "peak": FP64_PEAK_TFLOPS,
+                      "unit": "TFLOP/s", "frac": round(flops / (ms / 1e3) / 1e12 / FP64_PEAK_TFLOPS, 4),
+                      "traffic": None, "algorithmic_flops_per_step": flops,
+                      "note": "the update's f64 flops over the whole loop's time (quantize + solve + update)"}}
+    # byte check: rows are independent in the loop, so rows of expert 0 through the oracle's fixed-order loop are
+    # exact; the CPU baseline: the reference's CPU loop order, one expert's row sample a thread
     nthr = cpu_threads()
-    per = max(1, rows // nthr)
-    import concurrent.futures
-    t0 = time.time()
-    with concurrent.futures.ThreadPoolExecutor(nthr) as ex:
-        parts = list(ex.map(lambda r0: orc.ldlq(gpuq.IQ2_S, Wp_s[:, r0:r0 + per], U0, qw0, slots)[0],
-                            range(0, rows, per)))
-    cpu_s = time.time() - t0
-    want = np.concatenate(parts, axis=1)
-    e["sample_identical_to_oracle"] = bool(np.array_equal(out[0:1, :rows].cpu().numpy(), want))
+    check_rows = 16
+    U0 = Us[0].cpu().numpy()
+    qw_h = qw.cpu().numpy()
+    want = orc.ldlq(gpuq.IQ2_S, Wp0[0:1, :check_rows].cpu().numpy(), U0, qw_h[0:1], slots)[0]
+    e["sample_identical_to_oracle"] = bool(np.array_equal(out[0:1, :check_rows].cpu().numpy(), want))
     if want_cpu:
-        e["cpu_baseline"] = {"value": round(rows * ne0 / cpu_s / 1e6, 3), "unit": "Mweights/s", "cores": nthr,
-                             "kind": "port", "sample": "expert 0, %d rows (the loop's rows are independent), %.1f s "
-                                                       "on %d threads" % (rows, cpu_s, nthr)}
+        import concurrent.futures
+        from threadpoolctl import threadpool_limits
+        nexp_s = min(nexp_, nthr)
+        Uh = [U0] + [Us[i].cpu().numpy() for i in range(1, nexp_s)]
+
+        def cpu_pass(rows):
+            Ws = [Wp0[i, :rows].cpu().numpy() for i in range(nexp_s)]
+            t0 = time.time()
+            with threadpool_limits(limits=1), concurrent.futures.ThreadPoolExecutor(nthr) as ex:
+                res = list(ex.map(lambda i: blas_ldlq_rows(orc, gpuq.IQ2_S, Ws[i], Uh[i], qw_h[i]), range(nexp_s)))
+            return res, time.time() - t0
+        rows = 32
+        parts, cpu_s = cpu_pass(rows)
+        if cpu_s < CPU_MIN_S:                     # (a sample of about CPU_MIN_S: a stable rate)
+            rows = int(min(ne1, max(rows, rows * CPU_MIN_S / max(cpu_s, 1e-3))) // 16 * 16)
+            parts, cpu_s = cpu_pass(rows)
+        same = []
+        gpu_h = out[:nexp_s, :rows].cpu().numpy().reshape(nexp_s, rows, ne0 // 256, tsize)
+        for i, blocks in enumerate(parts):
+            for k, b in enumerate(blocks):
+                same.append((gpu_h[i][:, slots[k]] == b).all(axis=1))
+        share = float(np.concatenate(same).mean())
+        e["cpu_baseline"] = {"value": round(nexp_s * rows * ne0 / cpu_s / 1e6, 3), "unit": "Mweights/s",
+                             "cores": nthr, "cpu": cpu_model(), "kind": "port",
+                             "sample": "%d experts x %d rows (the loop's rows are independent), one expert a thread, "
+                                       "numpy LU solve + BLAS product a block (1 BLAS thread each) around the oracle's "
+                                       "IQ2_S quantizer and reader, %.1f s" % (nexp_s, rows, cpu_s)}
+        e["cpu_loop_identical_superblocks"] = round(share, 4)
         e["speedup_vs_cpu"] = round(e["value"] / e["cpu_baseline"]["value"], 1)
     del W, Us, Wp0, out
     torch.cuda.empty_cache()
@@ -301,17 +375,14 @@ def host_sample(torch, wl, rows):
     return wl.raw.reshape(-1)[: rows * wl.ncol // 32 * 17].cpu().numpy()
 
 
-def cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, wl, typ, ms, out_dev, sample_rows, want_cpu, tkey=None,
-                     tscale=1):
+def cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, wl, typ, ms, out_dev, sample_rows, want_cpu):
     """the CPU baseline on a sample, the op count per weight, and a byte spot check of the GPU output"""
-    import numpy as np
     nthr = cpu_threads()
     raw = host_sample(torch, wl, sample_rows)
     n = sample_rows * wl.ncol
     im = None
     if wl.imatrix is not None and typ != gpuq.Q8_0:
-        rows_per_mat = wl.nrow
-        nm = (sample_rows + rows_per_mat - 1) // rows_per_mat
+        nm = (sample_rows + wl.nrow - 1) // wl.nrow
         im = wl.imatrix[:nm].cpu().numpy()
     nmat_s, nrow_s = (sample_rows // wl.nrow, wl.nrow) if sample_rows >= wl.nrow else (1, sample_rows)
     entry = {}
@@ -330,20 +401,18 @@ def cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, wl, typ, ms, out_dev, sample
             cpu_s += time.time() - t0
             passes += 1
         entry["cpu_baseline"] = {"value": round(passes * n / cpu_s / 1e6, 2), "unit": "Mweights/s", "cores": nthr,
-                                 "kind": "port",
+                                 "cpu": cpu_model(), "kind": "port",
                                  "sample": "%d rows x %d of the same tensor (%.1f M weights), %d passes, %.1f s on %d "
                                            "threads" % (sample_rows, wl.ncol, n / 1e6, passes, cpu_s, nthr)}
     # roofline
-    n_total = wl.n
-    traffic = pmc_traffic(tkey)
-    if traffic is not None:
-        traffic *= tscale
+    key = "%s %s" % (gpuq.TYPE_NAMES[typ], wl.key)
+    traffic = pmc_traffic(key)
     if typ == gpuq.Q8_0:
         bpw = {0: 4.0, 30: 2.0}.get(wl.src, 17 / 32) + 34 / 32
-        achieved = bpw * n_total / (ms / 1e3) / 1e9
+        achieved = bpw * wl.n / (ms / 1e3) / 1e9
         entry["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                              "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                             "algorithmic_bytes_per_weight": bpw, "algorithmic_bytes": round(bpw * n_total)}
+                             "algorithmic_bytes_per_weight": bpw, "algorithmic_bytes": round(bpw * wl.n)}
     else:
         ops_rows = min(sample_rows, 64)
         sub = raw[: (ops_rows * wl.ncol) * {0: 4, 30: 2}.get(wl.src, 0)] if wl.src in (0, 30) else \
@@ -352,28 +421,50 @@ def cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, wl, typ, ms, out_dev, sample
         orc_ops.ops_read_reset()
         orc_ops.quantize(typ, f, None if im is None else im[0])
         opw = orc_ops.ops_read_reset() / (ops_rows * wl.ncol)
-        achieved = opw * n_total / (ms / 1e3) / 1e12
+        achieved = opw * wl.n / (ms / 1e3) / 1e12
         entry["roofline"] = {"bound": "valu", "achieved": round(achieved, 3), "peak": VALU_PEAK_TOPS,
                              "unit": "Tops/s", "frac": round(achieved / VALU_PEAK_TOPS, 4), "traffic": traffic,
                              "algorithmic_ops_per_weight": round(opw, 1)}
+        valu = pmc_valu(key)
+        if valu is not None:
+            entry["roofline"]["valu_issue"] = valu
     return entry
+
+
+def type_entry(torch, gq, gpuq, orc, orc_ops, wl, typ, steps, warmup, sample_rows, want_cpu):
+    ms, out = time_gpu(torch, gq, gpuq, wl, typ, steps, warmup)
+    e = {"workload": wl.name, "value": round(wl.n / (ms / 1e3) / 1e6, 1), "unit": "Mweights/s",
+         "ms_per_step": round(ms, 4), "steps": steps}
+    e.update(cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, wl, typ, ms, out, sample_rows, want_cpu))
+    if "cpu_baseline" in e:
+        e["speedup_vs_cpu"] = round(e["value"] / e["cpu_baseline"]["value"], 1)
+    return e, out
 
 
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--quick", action="store_true", help="headline workload only")
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--no-host", action="store_true",
                     help="skip the host entry point timings (their chunked launches would mix into a kernel profile)")
+    ap.add_argument("--only", default="", help="comma list of entries to run (%s, or an other type)" %
+                    ", ".join(ENTRIES))
     ap.add_argument("--experts", type=int, default=0, help="cap the expert count of the MoE workloads (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: there is no multi-GPU path (experts would shard across GPUs with no "
               "exchange step, each GPU writing disjoint byte ranges). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    only = [s.strip() for s in args.only.split(",") if s.strip()]
+    bad = [s for s in only if s not in ENTRIES + OTHER]
+    if bad:
+        ap.error("unknown --only entries: %s" % ", ".join(bad))
+
+    def want(name):
+        return not only or name in only
+
     import torch
     torch.cuda.init()
     import gpuq
@@ -382,96 +473,82 @@ def main():
     gq = gpuq.load_gpuq(0)
     orc = Oracle(tables=gpuq.tables_path())
     orc_ops = Oracle("liboracle_ops.so", tables=gpuq.tables_path())
-
-    # headline: Q4_K with imatrix on the 2048 x 7168 BF16 tensor
-    c2 = wl_c2(torch, gpuq)
-    log("headline: Q4_K on %s" % c2.name)
-    ms, out = time_gpu(torch, gq, gpuq, c2, gpuq.Q4_K, args.steps, args.warmup)
-    head = cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, c2, gpuq.Q4_K, ms, out, c2.nrow, not args.no_cpu,
-                            "Q4_K BF16 2048x7168")
-    value = c2.n / (ms / 1e3) / 1e6
-    line = {"metric": METRIC, "value": round(value, 1), "unit": "Mweights/s", "n_gpus": 1, "steps": args.steps,
-            "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
-            "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-            "config": {"workload": "Q4_K with imatrix, " + c2.name, "type": "Q4_K", "shape": [2048, 7168],
-                       "source": "BF16", "entry_point": "gpuq_requantize_dev"},
-            "roofline": head["roofline"]}
-    if "cpu_baseline" in head:
-        line["cpu_baseline"] = head["cpu_baseline"]
-    line["sample_identical_to_oracle"] = head["sample_identical_to_oracle"]
-    if not args.no_host:
-        log("host entry point: Q4_K on %s" % c2.name)
-        line["host_api"] = {"note": "PCIe-inclusive, pageable host memory in and out; not the value",
-                            "Q4_K": host_api(torch, gq, gpuq, c2, gpuq.Q4_K, 1, out)}
+    nthr = cpu_threads()
+    ksteps = max(1, min(args.steps, 5))
+    want_cpu = not args.no_cpu
+    line = {"metric": METRIC, "value": None, "unit": "Mweights/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f32", "data": "synthetic"}
+    host = {"note": "PCIe-inclusive, pageable host memory in and out; not the value"}
     per = {}
-    if not args.quick:
-        ksteps = max(1, min(args.steps, 5))
-        jobs = [("Q6_K", c2, gpuq.Q6_K, args.steps, c2.nrow)]
-        c1 = wl_c1(torch, gpuq)
-        jobs.insert(0, ("Q8_0", c1, gpuq.Q8_0, args.steps, c1.nrow))
-        for name, wl, typ, k, srows in jobs:
-            log("per type: %s on %s" % (name, wl.name))
-            ms_t, out_t = time_gpu(torch, gq, gpuq, wl, typ, k, args.warmup)
-            e = {"workload": wl.name, "value": round(wl.n / (ms_t / 1e3) / 1e6, 1), "unit": "Mweights/s",
-                 "ms_per_step": round(ms_t, 4), "steps": k}
-            e.update(cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, wl, typ, ms_t, out_t, srows, not args.no_cpu,
-                                      "%s %s" % (name, "F32 4096x4096" if wl is c1 else "BF16 2048x7168")))
-            per[name] = e
-            del out_t
-        del c1
-        # every other type on the same BF16 tensor: GPU rate, roofline (oracle-counted ops) and a byte spot check on
-        # 64 rows (no CPU timing)
-        other = {}
-        for name in ("Q2_K", "Q3_K", "Q5_K", "IQ4_NL", "IQ4_XS", "IQ2_XS", "IQ2_S", "IQ3_XXS", "IQ3_S"):
-            typ = getattr(gpuq, name)
-            log("other type: %s on %s" % (name, c2.name))
-            ms_t, out_t = time_gpu(torch, gq, gpuq, c2, typ, ksteps, 1)
-            e = {"value": round(c2.n / (ms_t / 1e3) / 1e6, 1), "unit": "Mweights/s", "ms_per_step": round(ms_t, 4),
-                 "steps": ksteps}
-            e.update(cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, c2, typ, ms_t, out_t, 64, False))
-            other[name] = e
-            del out_t
-        line["other_types"] = {"workload": c2.name, "types": other}
-        nthr = cpu_threads()
+
+    # headline: IQ2_XXS with imatrix on 256 BF16 experts of 2048 x 7168
+    if want("IQ2_XXS"):
         nexp_c3 = args.experts or 256
         c3 = wl_c3(torch, gpuq, nexp_c3)
-        for name, typ in (("IQ2_XXS", gpuq.IQ2_XXS),):
-            log("per type: %s on %s" % (name, c3.name))
-            ms_t, out_t = time_gpu(torch, gq, gpuq, c3, typ, ksteps, 1)
-            e = {"workload": c3.name, "value": round(c3.n / (ms_t / 1e3) / 1e6, 1), "unit": "Mweights/s",
-                 "ms_per_step": round(ms_t, 3), "steps": ksteps}
-            srows = c3.nrow * min(nexp_c3, max(2, nthr))
-            e.update(cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, c3, typ, ms_t, out_t, srows, not args.no_cpu,
-                                      "%s BF16 %dx2048x7168" % (name, c3.nmat)))
-            if "cpu_baseline" in e:
-                e["speedup_vs_cpu"] = round(e["value"] / e["cpu_baseline"]["value"], 1)
-            per[name] = e
-            if not args.no_host:
-                log("host entry point: %s on 16 experts" % name)
-                line["host_api"][name] = host_api(torch, gq, gpuq, c3, typ, min(16, c3.nmat), out_t)
-            del out_t
-        del c3
+        log("headline: IQ2_XXS on %s" % c3.name)
+        srows = c3.nrow * min(nexp_c3, max(2, nthr))
+        e, out = type_entry(torch, gq, gpuq, orc, orc_ops, c3, gpuq.IQ2_XXS, args.steps, args.warmup, srows,
+                            want_cpu)
+        line["value"] = e["value"]
+        line["ms_per_step"] = e["ms_per_step"]
+        line["config"] = {"workload": "IQ2_XXS with imatrix, " + c3.name, "type": "IQ2_XXS",
+                          "shape": [nexp_c3, 2048, 7168], "source": "BF16", "entry_point": "gpuq_requantize_dev"}
+        for k in ("roofline", "cpu_baseline", "speedup_vs_cpu", "sample_identical_to_oracle"):
+            if k in e:
+                line[k] = e[k]
+        if not args.no_host:
+            log("host entry point: IQ2_XXS on 16 experts")
+            host["IQ2_XXS"] = host_api(torch, gq, gpuq, c3, gpuq.IQ2_XXS, min(16, c3.nmat), out)
+        del c3, out
         torch.cuda.empty_cache()
+    if want("Q8_0"):
+        c1 = wl_c1(torch, gpuq)
+        log("per type: Q8_0 on %s" % c1.name)
+        per["Q8_0"], _ = type_entry(torch, gq, gpuq, orc, orc_ops, c1, gpuq.Q8_0, args.steps, args.warmup, c1.nrow,
+                                    want_cpu)
+        del c1
+    c2 = None
+    if want("Q4_K") or want("Q6_K") or any(want(t) for t in OTHER) or want("other"):
+        c2 = wl_c2(torch, gpuq)
+    for name in ("Q4_K", "Q6_K"):
+        if want(name):
+            log("per type: %s on %s" % (name, c2.name))
+            per[name], out = type_entry(torch, gq, gpuq, orc, orc_ops, c2, getattr(gpuq, name), args.steps,
+                                        args.warmup, c2.nrow, want_cpu)
+            if name == "Q4_K" and not args.no_host:
+                log("host entry point: Q4_K on %s" % c2.name)
+                host["Q4_K"] = host_api(torch, gq, gpuq, c2, gpuq.Q4_K, 1, out)
+            del out
+    other = {}
+    for name in OTHER:
+        if want(name) or (not only) or "other" in only:
+            log("other type: %s on %s" % (name, c2.name))
+            e, out = type_entry(torch, gq, gpuq, orc, orc_ops, c2, getattr(gpuq, name), ksteps, 1, 64, False)
+            del e["workload"]
+            other[name] = e
+            del out
+    if other:
+        line["other_types"] = {"workload": c2.name, "types": other}
+    del c2
+    if want("IQ1_S") or want("IQ1_M"):
         nexp_c4 = args.experts or 384
         c4 = wl_c4(torch, gpuq, nexp_c4)
-        for name, typ in (("IQ1_S", gpuq.IQ1_S), ("IQ1_M", gpuq.IQ1_M)):
-            log("per type: %s on %s" % (name, c4.name))
-            ms_t, out_t = time_gpu(torch, gq, gpuq, c4, typ, ksteps, 1)
-            e = {"workload": c4.name, "value": round(c4.n / (ms_t / 1e3) / 1e6, 1), "unit": "Mweights/s",
-                 "ms_per_step": round(ms_t, 3), "steps": ksteps}
-            srows = c4.nrow * min(nexp_c4, max(2, nthr))
-            e.update(cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, c4, typ, ms_t, out_t, srows, not args.no_cpu,
-                                      "%s MXFP4 %dx2048x7168" % (name, c4.nmat)))
-            if "cpu_baseline" in e:
-                e["speedup_vs_cpu"] = round(e["value"] / e["cpu_baseline"]["value"], 1)
-            per[name] = e
-            del out_t
+        for name in ("IQ1_S", "IQ1_M"):
+            if want(name):
+                log("per type: %s on %s" % (name, c4.name))
+                srows = c4.nrow * min(nexp_c4, max(2, nthr))
+                per[name], _ = type_entry(torch, gq, gpuq, orc, orc_ops, c4, getattr(gpuq, name), ksteps, 1, srows,
+                                          want_cpu)
         del c4
         torch.cuda.empty_cache()
+    if want("LDLQ"):
         log("per type: IQ2_S LDLQ")
-        per["IQ2_S_LDLQ"] = bench_ldlq(torch, gq, gpuq, orc, min(args.steps, 2), not args.no_cpu,
-                                       args.experts or 64)
+        per["IQ2_S_LDLQ"] = bench_ldlq(torch, gq, gpuq, orc, min(args.steps, 2), want_cpu, args.experts or 64)
+    if per:
         line["per_type"] = per
+    if len(host) > 1:
+        line["host_api"] = host
     print(json.dumps(line), flush=True)
 
 
