@@ -151,6 +151,7 @@ template <class T, int SRC> bool launch_q(const QParams &p, hipStream_t st) {
     const int64_t cap = (int64_t)g_ncu * 32 / wgw;          // 32 waves a CU in flight or queued
     if (wgs > cap) wgs = cap;
     if (wgs < 1) wgs = 1;
+    static_assert((size_t)T::TAB + wgw * wave_bytes<T>() <= 160 * 1024, "a workgroup's LDS within a CU's 160 KiB");
     const size_t lds = (size_t)T::TAB + wgw * wave_bytes<T>();
     hipLaunchKernelGGL((k_quant<T, SRC>), dim3((unsigned)wgs), dim3(64 * wgw), lds, st, p);
     return hipGetLastError() == hipSuccess;

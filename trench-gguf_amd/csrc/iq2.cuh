@@ -18,6 +18,7 @@
 #include <float.h>
 #include "kquants.cuh"
 #include "coop.cuh"
+#include "filter.cuh"
 
 #define EPS_IQ2S 1e-8f
 #define NKEY3 6561
@@ -158,18 +159,20 @@ DEV void sums_q8(const float *w, const float *xv, uint64_t pt, float &sumqx, flo
 // block: d qs[32] u16 (66 bytes); lane g = 32-weight sub-block g; q2[2g] at 2+8g, q2[2g+1] at 6+8g
 struct KIQ2XXS : Iq8Tab<256> {
     static constexpr int BS = QK, G = 8, N = 32, BB = 66, NTRIAL = 13;
-    static constexpr int MT = 4;        // trials searched by one wave-wide call
-    // per-wave LDS: the search workspace (the single-list and the MT-list searches share it and its staged values),
-    // then every trial's 4 grid indices (a u32 per trial and lane)
-    static constexpr int WSB = coop_wsm_bytes<MT>() > COOP_WS_BYTES ? coop_wsm_bytes<MT>() : COOP_WS_BYTES;
-    static constexpr int WS = WSB + NTRIAL * 64 * 4;
+    static constexpr int TW = 7;        // trials a window: windows 0..6 and 7..12
+    // per-wave LDS: the search workspace, shared by the filtered, the 4-list and the single-list searches and their
+    // staged values; eight waves a workgroup share one copy of the tables (the workspace would not let two four-wave
+    // workgroups share a CU's LDS)
+    static constexpr int WS0 = coop_wsm_bytes<4>() > COOP_WS_BYTES ? coop_wsm_bytes<4>() : COOP_WS_BYTES;
+    static constexpr int WS = (((int)sizeof(FiltWS<TW>) > WS0 ? (int)sizeof(FiltWS<TW>) : WS0) + 15) & ~15;
+    static constexpr int WGW = 8;
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
                           const QParams &p) {
         const uint64_t *grid = Iq8Tab<256>::grid(lds);
         const int32_t *map3 = Iq8Tab<256>::map3(lds);
         CoopWS &ws = *(CoopWS *)wave_ws<KIQ2XXS>(img);
-        CoopWSM<MT> &wsm = *(CoopWSM<MT> *)wave_ws<KIQ2XXS>(img);
-        uint32_t *gtab = (uint32_t *)(wave_ws<KIQ2XXS>(img) + WSB) + lane_id();   // [trial * 64]
+        CoopWSM<4> &wsm = *(CoopWSM<4> *)wave_ws<KIQ2XXS>(img);
+        FiltWS<TW> &fws = *(FiltWS<TW> *)wave_ws<KIQ2XXS>(img);
         float weight[N], xval[N];
         uint32_t bsg = 0;       // the 4 groups' 7-bit sign fields
         {
@@ -195,75 +198,126 @@ struct KIQ2XXS : Iq8Tab<256> {
             if (eff_max <= 0) scale = 0.f;
             else live = true;
         }
-        // The trials' groups, group by group (every lane runs them: the neighbour search is wave-wide): a group's
-        // values are staged once for its 13 trial scales, and trial t's grid index of group k goes to byte k of
-        // gtab[t]. Each trial's searches do not depend on another trial's outcome, so the order changes nothing.
-        float idv[NTRIAL], tsv[NTRIAL];         // the trial scales' inverse and scale, indexed by a uniform trial
-#pragma unroll
-        for (int t = 0; t < NTRIAL; ++t) {
-            idv[t] = (5 + (t - 6) * 0.1f) / eff_max;
-            tsv[t] = 1 / idv[t];
-        }
+        // The trials, a window of TW at a time (every lane runs them: the neighbour searches are wave-wide), group by
+        // group: a group's values are staged once for the window, each trial's key on the grid is its point, and the
+        // trials that share an off-grid key are searched by one filtered walk of its list (filter.cuh); a trial the
+        // filter leaves undecided goes through the exact search. The window's trials' sums of w*x*q and w*q*q
+        // gather group by group in index order, and the acceptance chain then runs over the window in ggml's order
+        // (each trial's searches do not depend on another trial's outcome, so this order changes nothing). The
+        // chain keeps the accepted trial (its number and scales), not its grid points.
+        float best = 0;
+        int tacc = -1;          // the last accepted trial (-1: none), its inverse scale and scale
+        float acc_id = 0.f, acc_sc = 0.f;
 #pragma unroll 1
-        for (int k = 0; k < 4; ++k) {           // (not unrolled: one copy of the search code, groups kept apart)
-            const float *xk = xval;            // group k: rotated to the front (rot8 below)
-            float waux[8];
+        for (int w0 = 0; w0 < NTRIAL; w0 += TW) {
+            float idv[TW], tsv[TW], sqx[TW], sq2[TW];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) waux[i] = sqrtf(weight[i]);
-            coop_stage<8>(ws, xk, waux);
+            for (int m = 0; m < TW; ++m) {
+                idv[m] = (5 + (w0 + m - 6) * 0.1f) / eff_max;
+                tsv[m] = 1 / idv[m];
+                sqx[m] = sq2[m] = 0.f;
+            }
 #pragma unroll 1
-            for (int t0 = 0; t0 < NTRIAL; t0 += MT) {
-                // trials t0 .. t0+MT-1: a key on the grid takes its point, the others search together; a search that
-                // accepts nothing flags the error (the reference traps) and yields 0
-                int mk[MT], cnt[MT], off[MT], gi[MT];
-                float tsc[MT];
+            for (int k = 0; k < 4; ++k) {       // (not unrolled: one copy of the search code, groups kept apart)
+                float xk[8], waux[8];           // group k: rotated to the front (rot8 below)
+                float sw = 0.f, swx = 0.f, swxx = 0.f;   // the filter's bound: sums of w, w|x|, w x^2
 #pragma unroll
-                for (int m = 0; m < MT; ++m) {
-                    const int t = t0 + m < NTRIAL ? t0 + m : NTRIAL - 1;
-                    const bool act = live && t0 + m < NTRIAL;
-                    mk[m] = act ? map3[group_key3(xk, idv[t])] : 0;
-                    off[m] = mk[m] < 0 ? m3_off(mk[m]) : 0;
-                    cnt[m] = mk[m] < 0 ? m3_cnt(mk[m]) : 0;
-                    tsc[m] = tsv[t];
+                for (int i = 0; i < 8; ++i) {
+                    xk[i] = xval[i];
+                    waux[i] = sqrtf(weight[i]);
+                    sw += waux[i];
+                    swx = fmaf(waux[i], fabsf(xk[i]), swx);
+                    swxx = fmaf(waux[i] * xk[i], xk[i], swxx);
                 }
-                coop_search_m<MT>(cnt, off, tsc, p.neigh, p.neigh_len, wsm, EvalIq8{grid}, gi);
+                // the window's keys; a list a run of equal off-grid keys (cnt > 0 at the run's first trial)
+                int mk[TW], cnt[TW], off[TW], ntr[TW];
 #pragma unroll
-                for (int m = 0; m < MT; ++m) {
-                    if (t0 + m < NTRIAL) {
-                        int g = mk[m];
-                        if (g < 0) {
-                            g = gi[m];
-                            if (g < 0) {
-                                flag_err(p);
-                                g = 0;
-                            }
-                        }
-                        ((uint8_t *)(gtab + (t0 + m) * 64))[k] = (uint8_t)g;
+                for (int m = 0; m < TW; ++m) mk[m] = live && w0 + m < NTRIAL ? map3[group_key3(xk, idv[m])] : 0;
+                {
+                    int run = 0;
+#pragma unroll
+                    for (int m = TW - 1; m >= 0; --m) {
+                        run = mk[m] < 0 ? (m + 1 < TW && mk[m + 1] == mk[m] ? run + 1 : 1) : 0;
+                        const bool head = mk[m] < 0 && (m == 0 || mk[m - 1] != mk[m]);
+                        cnt[m] = head ? m3_cnt(mk[m]) : 0;
+                        off[m] = head ? m3_off(mk[m]) : 0;
+                        ntr[m] = head ? run : 0;
                     }
                 }
-            }
-            rot8(xval);
-            rot8(weight);
-        }
-        // the acceptance chain over the trials, in ggml's order
-        float best = 0;
-        uint32_t P = 0;         // accepted trial's groups: grid indices, a byte each
-#pragma unroll 1
-        for (int t = 0; t < NTRIAL; ++t) {
-            const uint32_t Pa = gtab[t * 64];
-            float sumqx = 0, sumq2 = 0;
+                unsigned k1[TW], k2[TW];
+                coop_filter<TW, 8, 256>(cnt, off, ntr, tsv, xk, waux, p.neigh, p.neigh_len, fws, grid, k1, k2);
+                int gk[TW];             // the trials' grid indices of group k
+                unsigned amb = 0;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) sums_q8(weight + 8 * k, xval + 8 * k, grid[(Pa >> (8 * k)) & 255], sumqx, sumq2);
-            if (live && sumq2 > 0 && sumqx * sumqx > best * sumq2) {
-                scale = sumqx / sumq2;
-                best = scale * sumqx;
-                P = Pa;
+                for (int m = 0; m < TW; ++m) {
+                    gk[m] = mk[m] >= 0 ? mk[m] : filt_pick<8>(k1[m], k2[m], tsv[m], sw, swx, swxx);
+                    if (gk[m] < 0) amb |= 1u << m;
+                }
+                // the undecided trials, up to 4 a lane a call, through the exact search with the group's values
+                // staged (a search that accepts nothing flags the error, as the reference traps, and yields 0)
+                if (__ballot(amb != 0)) coop_stage<8>(ws, xk, waux);
+#pragma unroll 1
+                while (__ballot(amb != 0)) {
+                    int em[4], ecnt[4], eoff[4], egi[4];
+                    float esc[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        em[i] = amb ? __builtin_ctz(amb) : -1;
+                        amb &= amb - 1;
+                        int mv = 0;
+                        esc[i] = tsv[0];
+#pragma unroll
+                        for (int m = 0; m < TW; ++m) {
+                            if (m == em[i]) {
+                                mv = mk[m];
+                                esc[i] = tsv[m];
+                            }
+                        }
+                        ecnt[i] = em[i] >= 0 ? m3_cnt(mv) : 0;
+                        eoff[i] = em[i] >= 0 ? m3_off(mv) : 0;
+                    }
+                    coop_search_m<4>(ecnt, eoff, esc, p.neigh, p.neigh_len, wsm, EvalIq8{grid}, egi);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        if (em[i] >= 0) {
+                            int gv = egi[i];
+                            if (gv < 0) {
+                                flag_err(p);
+                                gv = 0;
+                            }
+#pragma unroll
+                            for (int m = 0; m < TW; ++m)
+                                if (m == em[i]) gk[m] = gv;
+                        }
+                    }
+                }
+#pragma unroll
+                for (int m = 0; m < TW; ++m) sums_q8(weight, xval, grid[gk[m]], sqx[m], sq2[m]);
+                rot8(xval);
+                rot8(weight);
+            }
+            // the acceptance chain over the window's trials, in ggml's order
+#pragma unroll
+            for (int m = 0; m < TW; ++m) {
+                if (w0 + m < NTRIAL && live && sq2[m] > 0 && sqx[m] * sqx[m] > best * sq2[m]) {
+                    scale = sqx[m] / sq2[m];
+                    best = scale * sqx[m];
+                    tacc = w0 + m;
+                    acc_id = idv[m];
+                    acc_sc = tsv[m];
+                }
             }
         }
-        // (after the trials scale > 0: either make_qp_quants' positive scale or an accepted positive one)
+        // The final pass at the chain's scale (after the trials scale > 0 unless the accepted trial's sum of w*x*q
+        // was negative: either make_qp_quants' positive scale or an accepted one). A lane whose chain ended on a
+        // negative scale keeps the accepted trial's grid points, found here again by the same searches at that
+        // trial's scales (none accepted: the points stay 0).
         const bool fin = live && scale > 0;
+        const bool alt = live && !fin && tacc >= 0;
+        uint32_t P = 0;
         {
-            const float id = 1 / scale;
+            const float id = fin ? 1 / scale : acc_id;
+            const float fsc = fin ? scale : acc_sc;
             uint32_t Pf = 0;
             float sumqx = 0, sumq2 = 0;
 #pragma unroll 1
@@ -272,16 +326,14 @@ struct KIQ2XXS : Iq8Tab<256> {
 #pragma unroll
                 for (int i = 0; i < 8; ++i) waux[i] = sqrtf(weight[i]);
                 bool og;
-                const int gi = group_point_w(fin, group_key3(xval, id), map3, p, grid, xval, waux, scale, ws, og);
+                const int gi = group_point_w(fin || alt, group_key3(xval, id), map3, p, grid, xval, waux, fsc, ws, og);
                 Pf |= (uint32_t)gi << (8 * k);
                 sums_q8(weight, xval, grid[gi], sumqx, sumq2);
                 rot8(xval);
                 rot8(weight);
             }
-            if (fin) {
-                P = Pf;
-                if (sumq2 > 0) scale = sumqx / sumq2;
-            }
+            if (fin || alt) P = Pf;
+            if (fin && sumq2 > 0) scale = sumqx / sumq2;
         }
         uint32_t q2lo = 0, q2hi = 0;
         if (live) {
