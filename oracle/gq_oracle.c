@@ -53,6 +53,14 @@ uint64_t gqo_ops_read_reset(void) { return 0; }
 
 static __thread int t_err;   /* a reference trap condition was hit in this thread */
 
+/* path counters: how often a quantization reached a case the GPU treats apart (see gq_oracle.h) */
+static uint64_t g_stat[GQO_NSTAT];
+#define STAT(i) __atomic_fetch_add(&g_stat[i], 1, __ATOMIC_RELAXED)
+uint64_t gqo_stat_read_reset(int which) {
+    if (which < 0 || which >= GQO_NSTAT) return 0;
+    return __atomic_exchange_n(&g_stat[which], 0, __ATOMIC_RELAXED);
+}
+
 /* ------------------------------------------------------------------ scalar helpers (gpuq/gpuq.hip:88-112, 2108-2121) */
 static inline uint32_t bits_of(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
 static inline float float_of(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
@@ -240,7 +248,7 @@ static float qp_levels(int n, int nmax, const float *x, uint8_t *L, const float 
 static int nb_iq2(const otab *t, const uint16_t *nb, const float *xv, const float *wa, float scale, int8_t *L) {
     const int cnt = nb[0];
     float best = FLT_MAX;
-    int gi = -1;
+    int gi = -1, nbest = 0;
     for (int j = 1; j <= cnt; ++j) {
         const int8_t *pg = grid_pt(t, nb[j]);
         float d2 = 0;
@@ -250,8 +258,11 @@ static int nb_iq2(const otab *t, const uint16_t *nb, const float *xv, const floa
             d2 += wa[i] * diff * diff;
         }
         OPS(8 * 6 + 3);
-        if (d2 < best) { best = d2; gi = nb[j]; }
+        if (d2 < best) { best = d2; gi = nb[j]; nbest = 1; }
+        else if (d2 == best) ++nbest;
     }
+    STAT(GQO_STAT_NB8_SEARCHES);
+    if (nbest > 1) STAT(GQO_STAT_NB8_TIES);
     if (gi < 0) { t_err = 1; gi = 0; }
     const int8_t *pg = grid_pt(t, gi);
     for (int i = 0; i < 8; ++i) L[i] = (int8_t)((pg[i] - 1) / 2);
@@ -416,6 +427,7 @@ static void o_iq2_xxs(const float *xbl, const float *qwbl, uint8_t *y, const ota
                 OPS(2 + C_DIV);
             }
         }
+        if (!(scale > 0)) STAT(GQO_STAT_IQ2XXS_NEGCHAIN);
         if (scale > 0) {
             const float id = 1 / scale;
             for (int k = 0; k < 4; ++k) {

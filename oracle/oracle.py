@@ -56,6 +56,8 @@ class Oracle:
         L.gqo_ldlq.argtypes = [ctypes.c_int, _vp, _vp, _vp, _i64, _i64, _i64, _vp, ctypes.c_int, _vp]
         L.gqo_schur_weights.argtypes = [_vp, _i64, _vp]
         L.gqo_ops_read_reset.restype = ctypes.c_uint64
+        L.gqo_stat_read_reset.restype = ctypes.c_uint64
+        L.gqo_stat_read_reset.argtypes = [ctypes.c_int]
         if tables is not None:
             rc = L.gqo_load_tables(tables.encode())
             if rc != 0:
@@ -134,3 +136,9 @@ class Oracle:
 
     def ops_read_reset(self):
         return self.lib.gqo_ops_read_reset()
+
+    STATS = {"nb8_searches": 0, "nb8_ties": 1, "iq2xxs_negchain": 2}
+
+    def stats_read_reset(self):
+        """the path counters (gq_oracle.h) since the last read, as a dict"""
+        return {k: self.lib.gqo_stat_read_reset(v) for k, v in self.STATS.items()}
