@@ -96,21 +96,20 @@ DEV int wave_incl_scan(int v) {
 // ev.point(idx): grid point idx (< 4096) as stored; ev(st, scale, pt): its distance for the owner's staged values st
 // (16 floats).
 //
-// The wave's 64*M lists are concatenated lane by lane, list by list (ids m*64 + lane), so M searches of every lane share one set-up
-// and one last, partly filled round. Rounds run in chunks of CH (8; fewer where lists are short): a first pass walks
-// the chunk's positions (list,
-// list position) and issues their list reads, a second reads their grid points, a third evaluates them, so a chunk's
-// reads are in flight together.
-// SLOTV: each slot's owner values and scale are read from LDS with its grid point, instead of once per list visited
-// into registers (for short lists, where a walker changes lists every few positions and the per-list read would
-// stall the evaluation that follows it).
-// A walker that has dealt with its own positions walks on through the following lists (the wave's last list links
-// to itself), so every slot holds a real candidate and needs no check: re-evaluating a candidate changes no minimum.
-// Along a walker's run a list's positions come in increasing order, so a strictly smaller distance alone keeps the
-// first of equal ones; the (distance, position) minimum across walkers is taken once per list visited.
-template <int M, int CH = 8, bool SLOTV = false, class Eval, int SW, bool PL, int NP>
+// The deal: each list is cut into pieces of CH consecutive candidates; the wave's pieces are concatenated lane by
+// lane, list by list (ids m*64 + lane, so M searches of every lane share one set-up and one last, partly filled
+// round), and walker L takes the contiguous run of R = ceil(pieces / 64) pieces from L*R, one a round. A walker
+// changes lists only between rounds, so the list changes (merge the running minimum, read the new owner's values and
+// scale) come once a round for the wave rather than at any position; within a round every walker evaluates the CH
+// candidates of one piece (positions past the list's end are masked). The next piece's list entries are read while
+// the current piece is evaluated. Along a walker's run a list's positions come in increasing order, so a strictly
+// smaller distance alone keeps the first of equal ones; the (distance, position) minimum across walkers is taken once
+// per list visited.
+template <int M, int CH = 4, class Eval, int SW, bool PL, int NP>
 DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&scale)[M], const uint16_t *neigh,
                        int neigh_len, CoopWSM<M, SW, PL, NP> &ws, const Eval &ev, int (&gi)[M]) {
+    static_assert(CH == 1 || CH == 2 || CH == 4 || CH == 8, "piece size: a power of two");
+    constexpr int CSH = CH == 1 ? 0 : CH == 2 ? 1 : CH == 4 ? 2 : 3;
     constexpr int ROWS = 64 * NP - 1;                   // list e's staged row: e & ROWS
     constexpr int OFF_MASK = (1 << 21) - 1;
     // the lists through a buffer resource: 32-bit offsets, and reads past the table return 0 instead of faulting
@@ -118,7 +117,7 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
     const int lane = lane_id();
     int tot = 0;
 #pragma unroll
-    for (int m = 0; m < M; ++m) tot += cnt[m];
+    for (int m = 0; m < M; ++m) tot += (cnt[m] + CH - 1) >> CSH;
     const int incl = wave_incl_scan(tot);
     const int total = __builtin_amdgcn_readlane(incl, 63);
 #pragma unroll
@@ -149,93 +148,96 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
             if (cnt[m] > 0) carry = e;
         }
     }
-    const int R = (total + 63) >> 6;                    // positions a lane
+    const int R = (total + 63) >> 6;                    // pieces a walker
     {
-        int start = incl - tot;                         // the list's first position
+        int start = incl - tot;                         // the list's first piece
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-            // walkers L with start <= L*R < start + cnt begin in list m (none when cnt == 0: lf > ll)
+            // walkers L with start <= L*R < start + np begin in list m (none when np == 0: lf > ll)
+            const int np = (cnt[m] + CH - 1) >> CSH;
             const int lf = div_small(start + R - 1, R);
-            const int ll = div_small(start + cnt[m] - 1, R);
+            const int ll = div_small(start + np - 1, R);
             for (int L = lf; L <= ll && L < 64; ++L)
                 ws.mark[L] = (m * 64 + lane) | (((int)__umul24((unsigned)L, (unsigned)R) - start) << 8);
-            start += cnt[m];
+            start += np;
         }
     }
     wave_sync();
-    // walk state: list, list position, the list's length and first entry, the next list's entry (read ahead)
+    const int p0 = (int)__umul24((unsigned)lane, (unsigned)R);   // this walker's first piece
+    // walk state: the piece's list, its piece number, the list's length and first entry, the next list's entry
     int o, j;
-    if (lane * R < total) {
+    if (p0 < total) {
         const int mk = ws.mark[lane];
         o = mk & 255;
         j = mk >> 8;
-    } else {                                            // (a walker with no positions starts on the last list)
+    } else {                                            // (a walker with no pieces starts on the last list)
         o = wlast;
         j = 0;
     }
-    const int2 oe = ws.ent[o];
-    int ocnt = oe.x >> 21;
-    int ol = oe.x & OFF_MASK;
-    int2 nx = ws.ent[oe.y & 255];
-    // evaluation state: the list being evaluated, its owner's values and scale, the best distance bits and position
-    int cur = o;
-    float st[16], sc = ws.esc[o];
-    unsigned bbits = ~0u;
-    int bown = 0, bidx = 0;
-    if (!SLOTV) coop_fetch(ws, o & ROWS, st);
-    for (int r0 = 0; r0 < R; r0 += CH) {
-        const int rend = R - r0 < CH ? R - r0 : CH;
-        int own_j[CH], idx[CH];         // list | list position << 8; the candidate's grid index
-        decltype(ev.point(0)) pt[CH];   // the candidate's grid point
-        // all CH slots walk and read, also past the last round (their candidates are real; only the rounds up to R
-        // are evaluated), so neither pass branches on the round count
-#pragma unroll
-        for (int r = 0; r < CH; ++r) {
-            if (j >= ocnt) {                            // the list ends: on to the next list with candidates
-                o = nx.y >> 8;
-                ol = nx.x & OFF_MASK;                   // (written in place: a temporary here could be a register
-                                                        // with a list read in flight, and wait for it)
-                ocnt = nx.x >> 21;
-                j = 0;
-                nx = ws.ent[nx.y & 255];
-            }
-            own_j[r] = o | (j << 8);
-            idx[r] = __builtin_amdgcn_raw_buffer_load_b16(nrs, (ol + j) * 2, 0, 0);
-            ++j;
-        }
-#pragma unroll
-        for (int r = 0; r < CH; ++r) pt[r] = ev.point(idx[r]);
-        float sv[SLOTV ? CH : 1][16], ss[SLOTV ? CH : 1];
-        if (SLOTV) {
-#pragma unroll
-            for (int r = 0; r < CH; ++r) {
-                const int e = own_j[r] & 255;
-                coop_fetch(ws, e & ROWS, sv[r]);
-                ss[r] = ws.esc[e];
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < CH; ++r) {
-            if (r < rend) {
-                const int e = own_j[r] & 255;
-                if (e != cur) {
-                    atomicMin(&ws.key[cur], ((unsigned long long)bbits << 32) | (unsigned)((bown >> 8) << 12 | bidx));
-                    if (!SLOTV) {
-                        if (NP == M || ((e ^ cur) & ROWS)) coop_fetch(ws, e & ROWS, st);
-                        sc = ws.esc[e];
-                    }
-                    cur = e;
-                    bbits = ~0u;
-                }
-                const unsigned b = __float_as_uint(SLOTV ? ev(sv[r], ss[r], pt[r]) : ev(st, sc, pt[r]));
-                const bool lt = b < bbits;              // (selects, not a branch)
-                bbits = lt ? b : bbits;
-                bown = lt ? own_j[r] : bown;
-                bidx = lt ? idx[r] : bidx;
-            }
-        }
+    int2 nx;
+    int ocnt, ol;
+    {
+        const int2 oe = ws.ent[o];
+        ocnt = oe.x >> 21;
+        ol = oe.x & OFF_MASK;
+        nx = ws.ent[oe.y & 255];
     }
-    atomicMin(&ws.key[cur], ((unsigned long long)bbits << 32) | (unsigned)((bown >> 8) << 12 | bidx));
+    // evaluation state: the list being evaluated, its owner's values and scale, the best distance bits and position
+    int cur = -1;
+    float st[16], sc = 0.f;
+    unsigned bbits = ~0u;
+    int bpos = 0, bidx = 0;
+    int idx[CH];
+#pragma unroll
+    for (int r = 0; r < CH; ++r) idx[r] = __builtin_amdgcn_raw_buffer_load_b16(nrs, (ol + (j << CSH) + r) * 2, 0, 0);
+    for (int rd = 0; rd < R; ++rd) {
+        // the next piece: the list's next, or the next list's first; its list entries read now
+        int o2 = o, j2 = j + 1, ocnt2 = ocnt, ol2 = ol;
+        int2 nx2 = nx;
+        if ((j2 << CSH) >= ocnt) {
+            o2 = nx.y >> 8;
+            ocnt2 = nx.x >> 21;
+            ol2 = nx.x & OFF_MASK;
+            j2 = 0;
+            nx2 = ws.ent[nx.y & 255];
+        }
+        int idx2[CH];
+        if (rd + 1 < R) {                               // (wave-uniform)
+#pragma unroll
+            for (int r = 0; r < CH; ++r)
+                idx2[r] = __builtin_amdgcn_raw_buffer_load_b16(nrs, (ol2 + (j2 << CSH) + r) * 2, 0, 0);
+        }
+        // a new list: merge the minimum of the last one, read the owner's values and scale
+        if (o != cur) {
+            if (cur >= 0) atomicMin(&ws.key[cur], ((unsigned long long)bbits << 32) | (unsigned)(bpos << 12 | bidx));
+            if (NP == M || cur < 0 || ((o ^ cur) & ROWS)) coop_fetch(ws, o & ROWS, st);
+            sc = ws.esc[o];
+            cur = o;
+            bbits = ~0u;
+        }
+        // this piece's candidates (positions past the list's end or pieces past the wave's total: no distance)
+        const bool pv = p0 + rd < total;
+        decltype(ev.point(0)) pt[CH];
+        bool v[CH];
+#pragma unroll
+        for (int r = 0; r < CH; ++r) {
+            v[r] = pv && (j << CSH) + r < ocnt;
+            pt[r] = ev.point(v[r] ? idx[r] : 0);        // (a masked position reads point 0)
+        }
+#pragma unroll
+        for (int r = 0; r < CH; ++r) {
+            const int pos = (j << CSH) + r;
+            const unsigned b = v[r] ? __float_as_uint(ev(st, sc, pt[r])) : ~0u;
+            const bool lt = b < bbits;                  // (selects, not a branch)
+            bbits = lt ? b : bbits;
+            bpos = lt ? pos : bpos;
+            bidx = lt ? idx[r] : bidx;
+        }
+        o = o2; j = j2; ocnt = ocnt2; ol = ol2; nx = nx2;
+#pragma unroll
+        for (int r = 0; r < CH; ++r) idx[r] = idx2[r];
+    }
+    atomicMin(&ws.key[cur], ((unsigned long long)bbits << 32) | (unsigned)(bpos << 12 | bidx));
     wave_sync();
     // the winners: a minimum at or above FLT_MAX (or NaN) is nothing accepted
 #pragma unroll
@@ -248,7 +250,7 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
 }
 
 // the search with one list a lane: returns gi (see coop_search_m)
-template <int CH = 8, class Eval>
+template <int CH = 4, class Eval>
 DEV int coop_search(int cnt, int off, float scale, const uint16_t *neigh, int neigh_len, CoopWS &ws,
                     const Eval &ev) {
     const int c[1] = {cnt}, o[1] = {off};

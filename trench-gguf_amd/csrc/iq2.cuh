@@ -73,7 +73,7 @@ struct EvalIq8 {
 // grid takes that point (og = true), the others search their neighbour lists together (coop_search) with the values
 // the caller staged (coop_stage). Inactive lanes get 0. A search that accepts nothing flags the error (the reference
 // traps) and yields 0.
-template <int CH = 8>
+template <int CH = 4>
 DEV int group_point_s(bool active, int k3, const int32_t *map3, const QParams &p, const uint64_t *grid, float scale,
                       CoopWS &ws, bool &og) {
     const int m = active ? map3[k3] : 0;
@@ -91,7 +91,7 @@ DEV int group_point_s(bool active, int k3, const int32_t *map3, const QParams &p
 }
 
 // the same, staging the group's values (x's xv, weights wa) first
-template <int CH = 8>
+template <int CH = 4>
 DEV int group_point_w(bool active, int k3, const int32_t *map3, const QParams &p, const uint64_t *grid,
                       const float *xv, const float *wa, float scale, CoopWS &ws, bool &og) {
     coop_stage<8>(ws, xv, wa);
@@ -362,10 +362,9 @@ struct KIQ2XXS : Iq8Tab<256> {
 // ------------------------------------------------------------------ IQ2_XS / IQ2_S: the 16-weight search
 // (gpuq/gpuq.hip:690-822, 824-969). Returns the sub-block scale; gidx the two grid indices, bsg the two sign bytes;
 // live = false for a skipped (negligible) sub-block.
-// IQ2_S's one-shell neighbour lists are short (3.4 points on average): its searches read each slot's owner values
-// with the slot (SLOTV) in chunks of 4 rounds (3% faster than per-list reads in chunks of 2); IQ2_XS's two-shell
-// lists are longer: per-list reads, 8 rounds a chunk (measured 3% faster than 2)
-template <int GRID> constexpr int ch16() { return GRID == 512 ? 8 : 4; }
+// The searches deal their lists in pieces of ch16 candidates: IQ2_S's one-shell lists hold 3.4 points on average
+// (pieces of 2 measured 2% faster than 4, 11% faster than 8), IQ2_XS's two-shell lists more (4: 6% faster than 2)
+template <int GRID> constexpr int ch16() { return GRID == 1024 ? 2 : 4; }
 // the search workspace of the 16-weight types: two trial scales of the lane's two groups as four lists (list
 // t*2 + k: trial t, group k), the two groups' values staged once (row k*64 + lane)
 using Iq16WS = CoopWSM<4, 16, true, 2>;
@@ -388,7 +387,7 @@ DEV void iq2_16_points(const bool (&act)[4], const float (&id)[2], const float (
         off[m] = act[m] && mk[m] < 0 ? m3_off(mk[m]) : 0;
         sc[m] = scale[m >> 1];
     }
-    coop_search_m<4, ch16<GRID>(), GRID == 1024>(cnt, off, sc, p.neigh, p.neigh_len, ws, EvalIq8{grid}, g);
+    coop_search_m<4, ch16<GRID>()>(cnt, off, sc, p.neigh, p.neigh_len, ws, EvalIq8{grid}, g);
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
         gi[m] = mk[m];

@@ -71,7 +71,7 @@ DEV int group_key8(const float *xv, float id) {
 }
 
 using Iq3WS = CoopWSM<4, 8, true>;
-constexpr int IQ3_CH = 4;       // rounds a chunk of the neighbour search
+constexpr int IQ3_CH = 4;       // the neighbour search's piece size (candidates a round)
 
 // The 8 groups' points of every lane at one scale (all lanes call it together): a group with act[k] takes the grid
 // point of its key (id) if the key is on the grid, else the winner of its neighbour list (the distances at `scale`);
