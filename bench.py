@@ -64,6 +64,9 @@ def profile_value(fname, tag, key):
     return None
 
 
+KEY_SUFFIX = ""        # appended to the profile keys of a run on other tables than the regular ones
+
+
 def pmc_traffic(key):
     """HBM bytes a launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on this workload, scaled by the same counters'
     reading for a copy kernel of known size (profiles/hbm_traffic_pmc.md), or None when not measured"""
@@ -404,8 +407,8 @@ def cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, wl, typ, ms, out_dev, sample
                                  "cpu": cpu_model(), "kind": "port",
                                  "sample": "%d rows x %d of the same tensor (%.1f M weights), %d passes, %.1f s on %d "
                                            "threads" % (sample_rows, wl.ncol, n / 1e6, passes, cpu_s, nthr)}
-    # roofline
-    key = "%s %s" % (gpuq.TYPE_NAMES[typ], wl.key)
+    # roofline (the counters in profiles/ are for the regular tables only)
+    key = "%s %s%s" % (gpuq.TYPE_NAMES[typ], wl.key, KEY_SUFFIX)
     traffic = pmc_traffic(key)
     if typ == gpuq.Q8_0:
         bpw = {0: 4.0, 30: 2.0}.get(wl.src, 17 / 32) + 34 / 32
@@ -452,6 +455,9 @@ def main():
     ap.add_argument("--only", default="", help="comma list of entries to run (%s, or an other type)" %
                     ", ".join(ENTRIES))
     ap.add_argument("--experts", type=int, default=0, help="cap the expert count of the MoE workloads (profiling)")
+    ap.add_argument("--tables", choices=["regular", "extreme"], default="regular",
+                    help="search tables: the regular stand-ins, or the extreme set (more neighbour shells: lists up to "
+                         "490 points) that bounds how the i-quant rates depend on the tables' shape")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: there is no multi-GPU path (experts would shard across GPUs with no "
@@ -471,14 +477,24 @@ def main():
     from oracle import Oracle
     os.environ["GPUQ_ALLOW_SYNTHETIC_TABLES"] = "1"      # the repository's stand-in IQ tables (a benchmark run)
     gq = gpuq.load_gpuq(0)
-    orc = Oracle(tables=gpuq.tables_path())
-    orc_ops = Oracle("liboracle_ops.so", tables=gpuq.tables_path())
+    tpath = gpuq.tables_path()
+    if args.tables == "extreme":
+        global KEY_SUFFIX
+        KEY_SUFFIX = " extreme tables"
+        tpath = os.path.join(os.path.dirname(tpath), "gpuq_tables_extreme.bin")
+        rc = gq.gpuq_init(tpath.encode(), 0)
+        if rc != 0:
+            sys.exit("gpuq_init %d on %s (built by __graft_entry__.build())" % (rc, tpath))
+    orc = Oracle(tables=tpath)
+    orc_ops = Oracle("liboracle_ops.so", tables=tpath)
     nthr = cpu_threads()
     ksteps = max(1, min(args.steps, 5))
     want_cpu = not args.no_cpu
     line = {"metric": METRIC, "value": None, "unit": "Mweights/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "f32", "data": "synthetic"}
+    if args.tables == "extreme":
+        line["tables"] = "gpuq_tables_extreme.bin (the stand-in grids with more neighbour shells)"
     host = {"note": "PCIe-inclusive, pageable host memory in and out; not the value"}
     per = {}
 

@@ -15,6 +15,7 @@
 #include <cstdlib>
 #include <mutex>
 #include <thread>
+#include <unordered_map>
 #include <vector>
 
 #include "common.cuh"
@@ -130,9 +131,48 @@ bool valid_search(int t, const std::vector<uint64_t> &grid, const std::vector<in
         if (off >= NL) return false;
         const int cnt = neigh[off];
         if (cnt < 1 || off + cnt >= NL) return false;
-        if (off + 1 >= (1 << M3_OFF_BITS) || cnt >= (1 << (31 - M3_OFF_BITS))) return false;
         for (int j = 1; j <= cnt; ++j)
             if (neigh[off + j] >= G) return false;
+    }
+    return true;
+}
+
+// The map the kernels stage and the neighbour lists they read, from a validated record: for the 8-value types the
+// map re-indexed by base-3 keys (6561; the trial rounding's levels are 0..2, so no other key is ever looked up), for
+// the 4-value types the 4096 3-bit keys as they are. Only the lists these keys reach are kept, in the file's layout
+// (a count, then the points), each once, in key order; an off-grid entry packs the list's offset in that buffer and
+// its length (m3_off / m3_cnt). False when a list's offset or length does not fit the packing (M3_OFF_BITS).
+bool pack_search(int t, const std::vector<int32_t> &map, const std::vector<uint16_t> &neigh,
+                 std::vector<int32_t> &m3, std::vector<uint16_t> &nb) {
+    const bool e8 = eight_values(t);
+    m3.assign(e8 ? 6561 : 4096, 0);
+    nb.clear();
+    std::unordered_map<int64_t, int> moved;             // file offset -> offset in nb
+    for (int k = 0; k < (int)m3.size(); ++k) {
+        int u = k, rr = k;
+        if (e8) {
+            u = 0;
+            for (int i = 0; i < 8; ++i) { u |= (rr % 3) << (2 * i); rr /= 3; }
+        }
+        const int m = map[u];
+        if (m >= 0) {
+            m3[k] = m;
+            continue;
+        }
+        const int64_t off = -(int64_t)m - 1;
+        const int cnt = neigh[off];
+        auto it = moved.find(off);
+        int noff;
+        if (it != moved.end()) {
+            noff = it->second;
+        } else {
+            noff = (int)nb.size();
+            if ((int64_t)noff + 1 + cnt > (int64_t)1 << 30) return false;
+            nb.insert(nb.end(), neigh.begin() + off, neigh.begin() + off + 1 + cnt);
+            moved.emplace(off, noff);
+        }
+        if (noff + 1 >= (1 << M3_OFF_BITS) || cnt >= (1 << (31 - M3_OFF_BITS))) return false;
+        m3[k] = -1 - (noff | (cnt << M3_OFF_BITS));
     }
     return true;
 }
@@ -527,7 +567,14 @@ extern "C" int gpuq_init(const char *tables, int device) {
     if (!g_err && hipMalloc((void **)&g_err, sizeof(int)) != hipSuccess) return 4;
     FILE *f = fopen(tables, "rb");
     if (!f) return 2;
-    struct Rec { int type; std::vector<uint64_t> grid; std::vector<int32_t> map; std::vector<uint16_t> neigh; };
+    struct Rec {
+        int type;
+        std::vector<uint64_t> grid;
+        std::vector<int32_t> map;
+        std::vector<uint16_t> neigh;
+        std::vector<int32_t> m3;        // (search types) the staged map and the lists it reaches: pack_search
+        std::vector<uint16_t> nb;
+    };
     std::vector<Rec> recs;
     int32_t hdr[4];
     while (fread(hdr, sizeof hdr, 1, f) == 1) {
@@ -535,7 +582,7 @@ extern "C" int gpuq_init(const char *tables, int device) {
             fclose(f);
             return 3;
         }
-        Rec r{hdr[0], std::vector<uint64_t>(hdr[1]), std::vector<int32_t>(hdr[2]), std::vector<uint16_t>(hdr[3])};
+        Rec r{hdr[0], std::vector<uint64_t>(hdr[1]), std::vector<int32_t>(hdr[2]), std::vector<uint16_t>(hdr[3]), {}, {}};
         if (fread(r.grid.data(), 8, hdr[1], f) != (size_t)hdr[1] || fread(r.map.data(), 4, hdr[2], f) != (size_t)hdr[2] ||
             fread(r.neigh.data(), 2, hdr[3], f) != (size_t)hdr[3]) {
             fclose(f);
@@ -546,7 +593,7 @@ extern "C" int gpuq_init(const char *tables, int device) {
     fclose(f);
     // validate everything before touching the device tables
     bool synthetic = false;
-    for (const Rec &r : recs) {
+    for (Rec &r : recs) {
         if (r.type == SYNTHETIC_MARK) {
             synthetic = true;
         } else if (r.type >= 1000) {
@@ -554,6 +601,7 @@ extern "C" int gpuq_init(const char *tables, int device) {
             if (t < 0 || t >= 64 || !is_search_type(t) || (int)r.grid.size() != expected_grid(t)) return 6;
         } else if (r.type >= 0 && r.type < 64 && is_search_type(r.type)) {
             if (!valid_search(r.type, r.grid, r.map, r.neigh)) return 6;
+            if (!pack_search(r.type, r.map, r.neigh, r.m3, r.nb)) return 6;
         }
     }
     // the tables of an earlier call are replaced (once no launch can read them any more)
@@ -575,27 +623,12 @@ extern "C" int gpuq_init(const char *tables, int device) {
             t.dq_size = (int)r.grid.size();
         } else if (r.type >= 0 && r.type < 64 && is_search_type(r.type)) {
             Tabs &t = g_tabs[r.type];
-            if (!upload(&t.grid, r.grid) || !upload(&t.map, r.map) || !upload(&t.neigh, r.neigh)) return 4;
+            if (!upload(&t.grid, r.grid) || !upload(&t.map, r.map) || !upload(&t.neigh, r.nb) ||
+                !upload(&t.map3, r.m3))
+                return 4;
             t.grid_size = (int)r.grid.size();
             t.map_size = (int)r.map.size();
-            t.neigh_len = (int)r.neigh.size();
-            {
-                // the map the kernels stage: for the 8-value types re-indexed by base-3 keys (6561), for the 4-value
-                // types the 4096 3-bit keys as they are; off-grid entries pack the list offset and its length
-                // (m3_off / m3_cnt), checked by valid_search
-                const bool e8 = eight_values(r.type);
-                std::vector<int32_t> m3(e8 ? 6561 : 4096);
-                for (int k = 0; k < (int)m3.size(); ++k) {
-                    int u = k, rr = k;
-                    if (e8) {
-                        u = 0;
-                        for (int i = 0; i < 8; ++i) { u |= (rr % 3) << (2 * i); rr /= 3; }
-                    }
-                    const int m = r.map[u];
-                    m3[k] = m >= 0 ? m : -1 - ((-m - 1) | ((int)r.neigh[-(int64_t)m - 1] << M3_OFF_BITS));
-                }
-                if (!upload(&t.map3, m3)) return 4;
-            }
+            t.neigh_len = (int)r.nb.size();
             t.ok = true;
         }
     }

@@ -104,10 +104,18 @@ def _neighbours(grid_lv, map_size, nval, bits, nwant, on_grid):
     return keys, lists
 
 
-def synthetic_tables():
-    """[(type, grid uint64[G], map int32[M], neighbours uint16[N])] in the reference writer's record order"""
+# the extreme set: the same grids and rule with more distance shells, so lists run long (up to 490 points) and the
+# file's list offsets pass 2^21 (IQ1_S: 3.2M entries), bounding how the search's cost and the loader's packing depend
+# on the tables' shape
+EXTREME_SHELLS = {IQ2_XXS: 5, IQ2_XS: 4, IQ1_S: 4, IQ2_S: 4, IQ3_XXS: 5, IQ3_S: 6}
+
+
+def synthetic_tables(shells=None):
+    """[(type, grid uint64[G], map int32[M], neighbours uint16[N])] in the reference writer's record order; shells:
+    {type: distance shells} replacing SPECS' (EXTREME_SHELLS for the extreme set)"""
     recs = []
     for typ, n, nlev, nval, nwant in SPECS:
+        nwant = (shells or {}).get(typ, nwant)
         bits = 2 if nval == 8 else 3
         map_size = MAP2 if nval == 8 else MAP3
         gkeys, glv = _grid(n, nlev, nval, bits, map_size)
@@ -189,4 +197,6 @@ def content_sha(path):
 
 if __name__ == "__main__":
     import sys
-    write_tables(sys.argv[1] if len(sys.argv) > 1 else "gpuq_tables.bin")
+    args = [a for a in sys.argv[1:] if a != "--extreme"]
+    write_tables(args[0] if args else "gpuq_tables.bin",
+                 synthetic_tables(EXTREME_SHELLS) if "--extreme" in sys.argv else None)
