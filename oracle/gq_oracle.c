@@ -287,6 +287,7 @@ static int nb_iq1(const otab *t, const uint16_t *nb, const float *xv, const floa
         OPS(8 * 7 + 2);
         if (d2 < best) { best = d2; gi = nb[j]; }
     }
+    if (gi >= 0 && best < 0) STAT(GQO_STAT_NB1_NEGATIVE);
     if (gi < 0) { t_err = 1; gi = 0; }
     const int8_t *pg = grid_pt(t, gi);
     for (int i = 0; i < 8; ++i) L[i] = (int8_t)((pg[i] - 1) / 2);

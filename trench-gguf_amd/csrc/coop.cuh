@@ -7,11 +7,14 @@
 //
 // A candidate's distance is computed from the owner's values exactly as the serial scan computes it (same operands,
 // same operation order), and each list's winner is the minimum of (distance bits, list position) over its
-// candidates, taken with LDS atomic mins. A distance is a sum of w*diff*diff terms from +0 with w >= 0 (or NaN
-// weights), so it is never negative and never -0: the unsigned order of its bits is the float order, with NaN above
-// +inf. The smallest position among equal distances is the serial scan's first-wins rule (it replaces only on a
-// strictly smaller distance), and a minimum at or above FLT_MAX is the serial scan accepting nothing (best starts at
-// FLT_MAX, strict <): the reference traps there, the caller flags it.
+// candidates, taken with LDS atomic mins. A distance is a sum of w*diff*diff terms from +0; with w >= 0 (or NaN
+// weights) it is never negative and never -0, so the unsigned order of its bits is the float order, with NaN above
+// +inf. Negative weights (ggml takes any importance) make negative distances, which the serial scan accepts like any
+// other: the searches of a wave with a negative staged weight (SIGNED) map each distance to an order-preserving key
+// instead (-0 read as +0, NaN above everything). The smallest position among equal distances is the serial scan's
+// first-wins rule (it replaces only on a strictly smaller distance), and a minimum at or above FLT_MAX is the serial
+// scan accepting nothing (best starts at FLT_MAX, strict <; NaN is never accepted): the reference traps there, the
+// caller flags it.
 //
 // The deal: the wave's lists occupy consecutive ranges of one concatenation (a wave prefix sum). With
 // R = ceil(total / 64) rounds, lane L takes the contiguous run of positions [L*R, L*R + R): mostly one list's
@@ -105,7 +108,14 @@ DEV int wave_incl_scan(int v) {
 // the current piece is evaluated. Along a walker's run a list's positions come in increasing order, so a strictly
 // smaller distance alone keeps the first of equal ones; the (distance, position) minimum across walkers is taken once
 // per list visited.
-template <int M, int CH = 4, class Eval, int SW, bool PL, int NP>
+// a distance's key in float order for any sign: -0 as +0, negatives below +0 in reverse bit order, NaN above all
+DEV unsigned signed_key(float d) {
+    const unsigned b = d == 0.f ? 0u : __float_as_uint(d);
+    const unsigned k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return d != d ? ~0u : k;
+}
+
+template <int M, int CH = 4, bool SIGNED = false, class Eval, int SW, bool PL, int NP>
 DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&scale)[M], const uint16_t *neigh,
                        int neigh_len, CoopWSM<M, SW, PL, NP> &ws, const Eval &ev, int (&gi)[M]) {
     static_assert(CH == 1 || CH == 2 || CH == 4 || CH == 8, "piece size: a power of two");
@@ -227,7 +237,8 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
 #pragma unroll
         for (int r = 0; r < CH; ++r) {
             const int pos = (j << CSH) + r;
-            const unsigned b = v[r] ? __float_as_uint(ev(st, sc, pt[r])) : ~0u;
+            const float dv = ev(st, sc, pt[r]);
+            const unsigned b = v[r] ? (SIGNED ? signed_key(dv) : __float_as_uint(dv)) : ~0u;
             const bool lt = b < bbits;                  // (selects, not a branch)
             bbits = lt ? b : bbits;
             bpos = lt ? pos : bpos;
@@ -240,22 +251,23 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
     atomicMin(&ws.key[cur], ((unsigned long long)bbits << 32) | (unsigned)(bpos << 12 | bidx));
     wave_sync();
     // the winners: a minimum at or above FLT_MAX (or NaN) is nothing accepted
+    constexpr unsigned KMAX = SIGNED ? 0xff7fffffu : 0x7f7fffffu;   // FLT_MAX's key
 #pragma unroll
     for (int m = 0; m < M; ++m) {
         if (cnt[m] > 0) {
             const unsigned long long k = ws.key[m * 64 + lane];
-            gi[m] = (unsigned)(k >> 32) >= 0x7f7fffffu ? -1 : (int)(k & 0xfffu);
+            gi[m] = (unsigned)(k >> 32) >= KMAX ? -1 : (int)(k & 0xfffu);
         }
     }
 }
 
 // the search with one list a lane: returns gi (see coop_search_m)
-template <int CH = 4, class Eval>
+template <int CH = 4, bool SIGNED = false, class Eval>
 DEV int coop_search(int cnt, int off, float scale, const uint16_t *neigh, int neigh_len, CoopWS &ws,
                     const Eval &ev) {
     const int c[1] = {cnt}, o[1] = {off};
     const float s[1] = {scale};
     int g[1];
-    coop_search_m<1, CH>(c, o, s, neigh, neigh_len, ws, ev, g);
+    coop_search_m<1, CH, SIGNED>(c, o, s, neigh, neigh_len, ws, ev, g);
     return g[0];
 }

@@ -57,7 +57,12 @@ DEV int iq1_group_point(bool live, int m, const float *xk, const float *wk, floa
     on_grid = !srch;
     const int cnt = srch ? m3_cnt(m) : 0, off = srch ? m3_off(m) : 0;
     if (srch) coop_stage<8>(ws, xk, wk);
-    const int gi = coop_search(cnt, off, minus ? -scale : scale, p.neigh, p.neigh_len, ws, EvalIq1{grid});
+    bool neg = false;                   // (a negative importance: distances of any sign, see coop.cuh)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) neg = neg || wk[i] < 0.f;
+    const float ssc = minus ? -scale : scale;
+    const int gi = __ballot(srch && neg) ? coop_search<4, true>(cnt, off, ssc, p.neigh, p.neigh_len, ws, EvalIq1{grid})
+                                         : coop_search(cnt, off, ssc, p.neigh, p.neigh_len, ws, EvalIq1{grid});
     if (!live) return 0;
     if (!srch) return m;
     if (gi < 0) {

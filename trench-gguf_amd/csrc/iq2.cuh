@@ -335,6 +335,31 @@ struct KIQ2XXS : Iq8Tab<256> {
             if (fin || alt) P = Pf;
             if (fin && sumq2 > 0) scale = sumqx / sumq2;
         }
+        // a lane with no positive scale and no accepted trial (non-finite values or importances) keeps
+        // make_qp_quants' levels (0..4), which ggml looks up in the full map: a key off the grid (or past the map)
+        // is its abort, flagged here
+        if (__ballot(live && !fin && tacc < 0)) {
+            Lv<N> Lq;
+            (void)qp_levels<N>(4, xval, Lq, weight);
+            uint32_t Pq = 0;
+            bool off = false;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                int u = 0;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) u |= (int)Lq.get(8 * k + i) << (2 * i);
+                int m = u < p.map_size ? p.map[u] : -1;
+                if (m < 0) {
+                    off = true;
+                    m = 0;
+                }
+                Pq |= (uint32_t)m << (8 * k);
+            }
+            if (live && !fin && tacc < 0) {
+                P = Pq;
+                if (off) flag_err(p);
+            }
+        }
         uint32_t q2lo = 0, q2hi = 0;
         if (live) {
             if (scale < 0) {
