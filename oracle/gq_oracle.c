@@ -53,11 +53,20 @@ uint64_t gqo_ops_read_reset(void) { return 0; }
 
 static __thread int t_err;   /* a reference trap condition was hit in this thread */
 
-/* path counters: how often a quantization reached a case the GPU treats apart (see gq_oracle.h) */
+/* path counters: how often a quantization reached a case the GPU treats apart (see gq_oracle.h); counted per
+ * thread (a shared counter would serialise the threads on one cache line) and added up at the end of every chunk */
 static uint64_t g_stat[GQO_NSTAT];
-#define STAT(i) __atomic_fetch_add(&g_stat[i], 1, __ATOMIC_RELAXED)
+static __thread uint64_t t_stat[GQO_NSTAT];
+#define STAT(i) (++t_stat[i])
+static void stat_flush(void) {
+    for (int i = 0; i < GQO_NSTAT; ++i) {
+        if (t_stat[i]) __atomic_fetch_add(&g_stat[i], t_stat[i], __ATOMIC_RELAXED);
+        t_stat[i] = 0;
+    }
+}
 uint64_t gqo_stat_read_reset(int which) {
     if (which < 0 || which >= GQO_NSTAT) return 0;
+    stat_flush();
     return __atomic_exchange_n(&g_stat[which], 0, __ATOMIC_RELAXED);
 }
 
@@ -1867,6 +1876,7 @@ size_t gqo_quantize_chunk(int type, const float *src, void *dst, int64_t start, 
             quant_block(type, x + ib * bs, imatrix ? imatrix + ib * bs : NULL, out + r * row_size + ib * bb, t);
     }
     ops_flush();
+    stat_flush();
     return t_err ? 0 : (size_t)nrows * row_size;
 }
 
@@ -2231,6 +2241,7 @@ static void *mt_worker(void *arg) {
     }
     free(buf);
     ops_flush();
+    stat_flush();
     return NULL;
 }
 
