@@ -569,6 +569,7 @@ static float iq2_16_search(const float *xb, const float *qw, float sigma2, int p
         }
     }
     const int n_off = (!on_grid[0]) + (!on_grid[1]);
+    if (!(scale > 0)) STAT(GQO_STAT_IQ2X16_NEGCHAIN);
     if (n_off > 0 && scale > 0) {
         const float id = 1 / scale;
         OPS(C_DIV);

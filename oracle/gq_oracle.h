@@ -75,8 +75,10 @@ uint64_t gqo_ops_read_reset(void);
  * those whose least distance is shared by two or more candidates (the first wins; the GPU's filtered search cannot
  * decide them and runs the exact search). IQ2XXS_NEGCHAIN: IQ2_XXS sub-blocks whose acceptance chain ends at a
  * scale that is not positive (the final pass is skipped and the accepted trial's points are kept). NB1_NEGATIVE:
- * IQ1 neighbour searches (iq1_find_best_neighbour2) whose chosen distance is negative (negative importances). */
-enum { GQO_STAT_NB8_SEARCHES, GQO_STAT_NB8_TIES, GQO_STAT_IQ2XXS_NEGCHAIN, GQO_STAT_NB1_NEGATIVE, GQO_NSTAT };
+ * IQ1 neighbour searches (iq1_find_best_neighbour2) whose chosen distance is negative (negative importances).
+ * IQ2X16_NEGCHAIN: IQ2_XS / IQ2_S sub-blocks whose acceptance chain ends at a scale that is not positive. */
+enum { GQO_STAT_NB8_SEARCHES, GQO_STAT_NB8_TIES, GQO_STAT_IQ2XXS_NEGCHAIN, GQO_STAT_NB1_NEGATIVE,
+       GQO_STAT_IQ2X16_NEGCHAIN, GQO_NSTAT };
 uint64_t gqo_stat_read_reset(int which);
 
 #ifdef __cplusplus

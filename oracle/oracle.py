@@ -137,7 +137,7 @@ class Oracle:
     def ops_read_reset(self):
         return self.lib.gqo_ops_read_reset()
 
-    STATS = {"nb8_searches": 0, "nb8_ties": 1, "iq2xxs_negchain": 2, "nb1_negative": 3}
+    STATS = {"nb8_searches": 0, "nb8_ties": 1, "iq2xxs_negchain": 2, "nb1_negative": 3, "iq2x16_negchain": 4}
 
     def stats_read_reset(self):
         """the path counters (gq_oracle.h) since the last read, as a dict"""

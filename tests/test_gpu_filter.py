@@ -1,5 +1,6 @@
-"""IQ2_XXS's filtered neighbour search (csrc/filter.cuh) on inputs built to reach the cases it hands elsewhere,
-against the oracle byte for byte:
+"""The filtered neighbour search of IQ2_XXS and IQ2_XS (csrc/filter.cuh, window_group in csrc/iq2.cuh) on inputs
+built to reach the cases it hands elsewhere, against the oracle byte for byte (IQ2_S, whose searches are exact, on
+the same inputs):
 
 - exact ties between candidates (the least distance shared): the filter's margin test cannot decide them and the
   exact cooperative search repeats ggml's first-wins scan (|x| equal within a row, weights equal or zero, so
@@ -14,7 +15,9 @@ test compares the library's bytes with the oracle's on the same inputs."""
 import numpy as np
 import pytest
 
-IQ2_XXS, F32 = 16, 0
+IQ2_XXS, IQ2_XS, IQ2_S, F32 = 16, 17, 22, 0
+TYPES = {16: "iq2_xxs", 17: "iq2_xs", 22: "iq2_s"}
+NEGCHAIN = {16: "iq2xxs_negchain", 17: "iq2x16_negchain"}  # (IQ2_S keeps each sign: no flipped value)
 
 
 def negchain(nrow=16, ncol=2048, seed=0):
@@ -49,36 +52,40 @@ def magnitudes(nrow=16, ncol=2048, seed=2):
 CASES = {"negchain": negchain, "symmetric": symmetric, "magnitudes": magnitudes}
 
 
-def test_constructions_reach_their_cases(oracle_lib):
-    want = {"negchain": ("iq2xxs_negchain", 0), "symmetric": ("nb8_ties", 0), "magnitudes": ("nb8_searches", 0)}
+@pytest.mark.parametrize("typ", sorted(TYPES), ids=[TYPES[t] for t in sorted(TYPES)])
+def test_constructions_reach_their_cases(oracle_lib, typ):
+    bb = {16: 66, 17: 74, 22: 82}[typ]
+    want = {"negchain": NEGCHAIN.get(typ, "nb8_ties"), "symmetric": "nb8_ties", "magnitudes": "nb8_searches"}
     for name, make in CASES.items():
         x, im = make()
         oracle_lib.stats_read_reset()
-        q = oracle_lib.quantize(IQ2_XXS, x, im)
+        q = oracle_lib.quantize(typ, x, im)
         st = oracle_lib.stats_read_reset()
-        assert q.size == x.size // 256 * 66, name                 # (no trap: every search accepted a point)
-        key, floor = want[name]
-        assert st[key] > floor, (name, st)
-    x, im = negchain()
-    oracle_lib.stats_read_reset()
-    oracle_lib.quantize(IQ2_XXS, x, im)
-    st = oracle_lib.stats_read_reset()
-    assert st["iq2xxs_negchain"] >= x.size // 32 // 4 and st["nb8_ties"] > st["nb8_searches"] // 2, st
+        assert q.size == x.size // 256 * bb, name                 # (no trap: every search accepted a point)
+        assert st[want[name]] > 0, (name, st)
+    if typ in NEGCHAIN:
+        x, im = negchain()
+        oracle_lib.stats_read_reset()
+        oracle_lib.quantize(typ, x, im)
+        st = oracle_lib.stats_read_reset()
+        per = 32 if typ == 16 else 16                           # (weights a sub-block)
+        assert st[NEGCHAIN[typ]] >= x.size // per // 8 and st["nb8_ties"] > st["nb8_searches"] // 2, st
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("typ", sorted(TYPES), ids=[TYPES[t] for t in sorted(TYPES)])
 @pytest.mark.parametrize("name", sorted(CASES))
-def test_filter_cases_match_oracle(oracle_lib, name):
+def test_filter_cases_match_oracle(oracle_lib, name, typ):
     import torch
     import gpuq
     gq = gpuq.load_gpuq(0)
     x, im = CASES[name]()
-    want = oracle_lib.quantize(IQ2_XXS, x, im).reshape(-1)
+    want = oracle_lib.quantize(typ, x, im).reshape(-1)
     d_x = torch.from_numpy(x).cuda()
     d_im = torch.from_numpy(im).cuda()
     d_out = torch.zeros(want.size, dtype=torch.uint8, device="cuda")
-    print("case filter %s" % name, flush=True)
-    got = gq.gpuq_requantize_dev(F32, d_x.data_ptr(), IQ2_XXS, d_out.data_ptr(), 1, x.shape[0], x.shape[1],
+    print("case filter %s %s" % (TYPES[typ], name), flush=True)
+    got = gq.gpuq_requantize_dev(F32, d_x.data_ptr(), typ, d_out.data_ptr(), 1, x.shape[0], x.shape[1],
                                  d_im.data_ptr(), torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     assert got == want.size

@@ -155,6 +155,90 @@ DEV void sums_q8(const float *w, const float *xv, uint64_t pt, float &sumqx, flo
     }
 }
 
+// One group's trials of a window (every lane of the wave calls it together: the searches are wave-wide). xk, waux:
+// the group's 8 values and search weights; trial m's inverse scale idv[m] and scale tsv[m]; valid: the trials that
+// run (bit m; none for a lane that is not live). Trial m's key at idv[m]: on the grid its point; the runs of trials
+// with one off-grid key are searched by one filtered walk of the key's list (filter.cuh), and a trial the filter leaves
+// undecided goes through the exact search, up to 4 a lane a call (a search that accepts nothing flags the error, as
+// the reference traps, and yields 0). gk[m]: trial m's grid index (0 for a trial that does not run); og: bit m set
+// where trial m's key is on the grid (and for a trial that does not run). IB, NG: the grid indices' bits and the
+// grid's size. The staged area of fws, ws and wsm is one (the caller's workspace).
+template <int TW, int IB, int NG>
+DEV void window_group(const float (&xk)[8], const float (&waux)[8], const float (&idv)[TW], const float (&tsv)[TW],
+                      unsigned valid, const int32_t *map3, const QParams &p, const uint64_t *grid, FiltWS<TW> &fws,
+                      CoopWS &ws, CoopWSM<4> &wsm, int (&gk)[TW], unsigned &og) {
+    float sw = 0.f, swx = 0.f, swxx = 0.f;      // the filter's bound: sums of w, w|x|, w x^2
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        sw += waux[i];
+        swx = fmaf(waux[i], fabsf(xk[i]), swx);
+        swxx = fmaf(waux[i] * xk[i], xk[i], swxx);
+    }
+    // the window's keys; a list a run of equal off-grid keys (cnt > 0 at the run's first trial)
+    int mk[TW], cnt[TW], off[TW], ntr[TW];
+    og = 0;
+#pragma unroll
+    for (int m = 0; m < TW; ++m) {
+        mk[m] = (valid >> m) & 1 ? map3[group_key3(xk, idv[m])] : 0;
+        if (mk[m] >= 0) og |= 1u << m;
+    }
+    {
+        int run = 0;
+#pragma unroll
+        for (int m = TW - 1; m >= 0; --m) {
+            run = mk[m] < 0 ? (m + 1 < TW && mk[m + 1] == mk[m] ? run + 1 : 1) : 0;
+            const bool head = mk[m] < 0 && (m == 0 || mk[m - 1] != mk[m]);
+            cnt[m] = head ? m3_cnt(mk[m]) : 0;
+            off[m] = head ? m3_off(mk[m]) : 0;
+            ntr[m] = head ? run : 0;
+        }
+    }
+    unsigned k1[TW], k2[TW];
+    coop_filter<TW, IB, NG>(cnt, off, ntr, tsv, xk, waux, p.neigh, p.neigh_len, fws, grid, k1, k2);
+    unsigned amb = 0;
+#pragma unroll
+    for (int m = 0; m < TW; ++m) {
+        gk[m] = mk[m] >= 0 ? mk[m] : filt_pick<IB>(k1[m], k2[m], tsv[m], sw, swx, swxx);
+        if (gk[m] < 0) amb |= 1u << m;
+    }
+    if (__ballot(amb != 0)) coop_stage<8>(ws, xk, waux);
+#pragma unroll 1
+    while (__ballot(amb != 0)) {
+        int em[4], ecnt[4], eoff[4], egi[4];
+        float esc[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            em[i] = amb ? __builtin_ctz(amb) : -1;
+            amb &= amb - 1;
+            int mv = 0;
+            esc[i] = tsv[0];
+#pragma unroll
+            for (int m = 0; m < TW; ++m) {
+                if (m == em[i]) {
+                    mv = mk[m];
+                    esc[i] = tsv[m];
+                }
+            }
+            ecnt[i] = em[i] >= 0 ? m3_cnt(mv) : 0;
+            eoff[i] = em[i] >= 0 ? m3_off(mv) : 0;
+        }
+        coop_search_m<4>(ecnt, eoff, esc, p.neigh, p.neigh_len, wsm, EvalIq8{grid}, egi);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (em[i] >= 0) {
+                int gv = egi[i];
+                if (gv < 0) {
+                    flag_err(p);
+                    gv = 0;
+                }
+#pragma unroll
+                for (int m = 0; m < TW; ++m)
+                    if (m == em[i]) gk[m] = gv;
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------------ IQ2_XXS (gpuq/gpuq.hip:245-387)
 // block: d qs[32] u16 (66 bytes); lane g = 32-weight sub-block g; q2[2g] at 2+8g, q2[2g+1] at 6+8g
 struct KIQ2XXS : Iq8Tab<256> {
@@ -217,80 +301,21 @@ struct KIQ2XXS : Iq8Tab<256> {
                 tsv[m] = 1 / idv[m];
                 sqx[m] = sq2[m] = 0.f;
             }
+            unsigned valid = 0;
+#pragma unroll
+            for (int m = 0; m < TW; ++m)
+                if (live && w0 + m < NTRIAL) valid |= 1u << m;
 #pragma unroll 1
             for (int k = 0; k < 4; ++k) {       // (not unrolled: one copy of the search code, groups kept apart)
                 float xk[8], waux[8];           // group k: rotated to the front (rot8 below)
-                float sw = 0.f, swx = 0.f, swxx = 0.f;   // the filter's bound: sums of w, w|x|, w x^2
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     xk[i] = xval[i];
                     waux[i] = sqrtf(weight[i]);
-                    sw += waux[i];
-                    swx = fmaf(waux[i], fabsf(xk[i]), swx);
-                    swxx = fmaf(waux[i] * xk[i], xk[i], swxx);
                 }
-                // the window's keys; a list a run of equal off-grid keys (cnt > 0 at the run's first trial)
-                int mk[TW], cnt[TW], off[TW], ntr[TW];
-#pragma unroll
-                for (int m = 0; m < TW; ++m) mk[m] = live && w0 + m < NTRIAL ? map3[group_key3(xk, idv[m])] : 0;
-                {
-                    int run = 0;
-#pragma unroll
-                    for (int m = TW - 1; m >= 0; --m) {
-                        run = mk[m] < 0 ? (m + 1 < TW && mk[m + 1] == mk[m] ? run + 1 : 1) : 0;
-                        const bool head = mk[m] < 0 && (m == 0 || mk[m - 1] != mk[m]);
-                        cnt[m] = head ? m3_cnt(mk[m]) : 0;
-                        off[m] = head ? m3_off(mk[m]) : 0;
-                        ntr[m] = head ? run : 0;
-                    }
-                }
-                unsigned k1[TW], k2[TW];
-                coop_filter<TW, 8, 256>(cnt, off, ntr, tsv, xk, waux, p.neigh, p.neigh_len, fws, grid, k1, k2);
-                int gk[TW];             // the trials' grid indices of group k
-                unsigned amb = 0;
-#pragma unroll
-                for (int m = 0; m < TW; ++m) {
-                    gk[m] = mk[m] >= 0 ? mk[m] : filt_pick<8>(k1[m], k2[m], tsv[m], sw, swx, swxx);
-                    if (gk[m] < 0) amb |= 1u << m;
-                }
-                // the undecided trials, up to 4 a lane a call, through the exact search with the group's values
-                // staged (a search that accepts nothing flags the error, as the reference traps, and yields 0)
-                if (__ballot(amb != 0)) coop_stage<8>(ws, xk, waux);
-#pragma unroll 1
-                while (__ballot(amb != 0)) {
-                    int em[4], ecnt[4], eoff[4], egi[4];
-                    float esc[4];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        em[i] = amb ? __builtin_ctz(amb) : -1;
-                        amb &= amb - 1;
-                        int mv = 0;
-                        esc[i] = tsv[0];
-#pragma unroll
-                        for (int m = 0; m < TW; ++m) {
-                            if (m == em[i]) {
-                                mv = mk[m];
-                                esc[i] = tsv[m];
-                            }
-                        }
-                        ecnt[i] = em[i] >= 0 ? m3_cnt(mv) : 0;
-                        eoff[i] = em[i] >= 0 ? m3_off(mv) : 0;
-                    }
-                    coop_search_m<4>(ecnt, eoff, esc, p.neigh, p.neigh_len, wsm, EvalIq8{grid}, egi);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        if (em[i] >= 0) {
-                            int gv = egi[i];
-                            if (gv < 0) {
-                                flag_err(p);
-                                gv = 0;
-                            }
-#pragma unroll
-                            for (int m = 0; m < TW; ++m)
-                                if (m == em[i]) gk[m] = gv;
-                        }
-                    }
-                }
+                int gk[TW];                     // the trials' grid indices of group k
+                unsigned og;
+                window_group<TW, 8, 256>(xk, waux, idv, tsv, valid, map3, p, grid, fws, ws, wsm, gk, og);
 #pragma unroll
                 for (int m = 0; m < TW; ++m) sums_q8(weight, xval, grid[gk[m]], sqx[m], sq2[m]);
                 rot8(xval);
@@ -390,6 +415,7 @@ struct KIQ2XXS : Iq8Tab<256> {
 // The searches deal their lists in pieces of ch16 candidates: IQ2_S's one-shell lists hold 3.4 points on average
 // (pieces of 2 measured 2% faster than 4, 11% faster than 8), IQ2_XS's two-shell lists more (4: 6% faster than 2)
 template <int GRID> constexpr int ch16() { return GRID == 1024 ? 2 : 4; }
+constexpr int IQ2XS_TW = 7;     // IQ2_XS's trial window (filtered search)
 // the search workspace of the 16-weight types: two trial scales of the lane's two groups as four lists (list
 // t*2 + k: trial t, group k), the two groups' values staged once (row k*64 + lane)
 using Iq16WS = CoopWSM<4, 16, true, 2>;
@@ -449,6 +475,80 @@ DEV float iq2_16_search(const float (&x)[16], const float (&qv)[16], float sigma
     float scale = mx / 5;
     int P[2] = {-1, -1};        // accepted trial's groups as grid indices; -1: all levels 0 (no trial accepted yet)
     bool on_grid[2] = {true, true};
+    if constexpr (GRID == 512) {
+        // IQ2_XS (two-shell lists, 12.9 points on average): the 19 trials in windows of TW, group by group, through
+        // the filtered search (window_group), and the acceptance chain over each window from the trials' running
+        // sums; the chain keeps the accepted trial (number, scales, which groups were on the grid), and the pass
+        // below finds its points again: on the grid from their keys, off the grid by the same searches (IQ2_XXS's
+        // scheme, KIQ2XXS::quant)
+        constexpr int TW = IQ2XS_TW, NT = 19;
+        FiltWS<TW> &fws = *(FiltWS<TW> *)&ws;
+        CoopWS &ws1 = *(CoopWS *)&ws;
+        CoopWSM<4> &wsm = *(CoopWSM<4> *)&ws;
+        int tacc = -1;
+        float acc_id = 0.f, acc_sc = 0.f;
+        unsigned acc_og = 3u;
+#pragma unroll 1
+        for (int w0 = 0; w0 < NT; w0 += TW) {
+            float idv[TW], tsv[TW], sqx[TW], sq2[TW];
+            unsigned valid = 0;
+#pragma unroll
+            for (int m = 0; m < TW; ++m) {
+                idv[m] = (5 + (w0 + m - 9) * 0.1f) / mx;
+                tsv[m] = 1 / idv[m];
+                sqx[m] = sq2[m] = 0.f;
+                if (live && w0 + m < NT) valid |= 1u << m;
+            }
+            unsigned ogk[2];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                float xk[8], wk[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    xk[i] = xval[8 * k + i];
+                    wk[i] = waux[8 * k + i];
+                }
+                int gk[TW];
+                window_group<TW, 9, 512>(xk, wk, idv, tsv, valid, map3, p, grid, fws, ws1, wsm, gk, ogk[k]);
+#pragma unroll
+                for (int m = 0; m < TW; ++m) sums_q8(weight + 8 * k, xval + 8 * k, grid[gk[m]], sqx[m], sq2[m]);
+            }
+#pragma unroll
+            for (int m = 0; m < TW; ++m) {
+                if (w0 + m < NT && live && sq2[m] > 0 && sqx[m] * sqx[m] > best * sq2[m]) {
+                    scale = sqx[m] / sq2[m];
+                    best = scale * sqx[m];
+                    tacc = w0 + m;
+                    acc_id = idv[m];
+                    acc_sc = tsv[m];
+                    acc_og = ((ogk[0] >> m) & 1u) | (((ogk[1] >> m) & 1u) << 1);
+                }
+            }
+        }
+        on_grid[0] = (acc_og & 1u) != 0;
+        on_grid[1] = (acc_og & 2u) != 0;
+        // (a group left at levels 0 is on the grid: on_grid stays true for it)
+        const bool fin = live && (!on_grid[0] || !on_grid[1]) && scale > 0;
+        const bool alt = live && !fin && tacc >= 0;        // the accepted trial's points, found again
+#pragma unroll
+        for (int k = 0; k < 2; ++k) coop_stage<8>(ws, xval + 8 * k, waux + 8 * k, k * 64 + lane_id());
+        {
+            const float idf = fin ? 1 / scale : acc_id, scf = fin ? scale : acc_sc;
+            const float id[2] = {idf, idf}, fsc[2] = {scf, scf};
+            const bool act[4] = {(fin || alt) && !on_grid[0], (fin || alt) && !on_grid[1], false, false};
+            int gi[4];
+            bool og[4];
+            iq2_16_points<GRID>(act, id, fsc, xval, map3, p, grid, ws, gi, og);
+            float sumqx = 0, sumq2 = 0;
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                if (act[k]) P[k] = gi[k];
+                else if (tacc >= 0) P[k] = map3[group_key3(xval + 8 * k, acc_id)];   // (on the grid)
+                sums_q8(weight + 8 * k, xval + 8 * k, grid[P[k] < 0 ? 0 : P[k]], sumqx, sumq2);
+            }
+            if (fin && sumq2 > 0) scale = sumqx / sumq2;
+        }
+    } else {
     // the two groups' values, staged once for all the trials and the final pass
 #pragma unroll
     for (int k = 0; k < 2; ++k) coop_stage<8>(ws, xval + 8 * k, waux + 8 * k, k * 64 + lane_id());
@@ -496,6 +596,7 @@ DEV float iq2_16_search(const float (&x)[16], const float (&qv)[16], float sigma
             sums_q8(weight + 8 * k, xval + 8 * k, grid[P[k] < 0 ? 0 : P[k]], sumqx, sumq2);
         }
         if (fin && sumq2 > 0) scale = sumqx / sumq2;
+    }
     }
     if (!live) return 0.f;
     if (scale < 0) {
@@ -550,7 +651,9 @@ struct KIQ2S : Iq8Tab<1024> {
 
 // IQ2_XS: block d qs[32] u16 scales[8] (74 bytes); qs[2g+k] = grid index | signs << 9
 struct KIQ2XS : Iq8Tab<512> {
-    static constexpr int BS = QK, G = 16, N = 16, BB = 74, WS = coop_wsm_bytes<4, 16, true, 2>(), WGW = 8;
+    static constexpr int WS0 = coop_wsm_bytes<4, 16, true, 2>();
+    static constexpr int BS = QK, G = 16, N = 16, BB = 74, WGW = 8,
+                         WS = (((int)sizeof(FiltWS<IQ2XS_TW>) > WS0 ? (int)sizeof(FiltWS<IQ2XS_TW>) : WS0) + 15) & ~15;
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
                           const QParams &p) {
         float qv[N], sq[N];
