@@ -72,6 +72,25 @@ DEV int iq1_group_point(bool live, int m, const float *xk, const float *wk, floa
     return gi;
 }
 
+// Whether IQ1_S's partition scan may drop its `sumq2 > 0` test: a candidate's sumq2 is
+// a_w x0^2 + (s2w - s1w) x1^2 + (totw - s2w) x2^2 over the weights' prefix sums, three terms >= 0 that split totw, so
+// with every weight 0 or in [2^-100, 2^100] (no underflow or overflow on the way) it is > 0 exactly when the block's
+// weights are not all 0, and a block of zero weights never accepts. The test is dropped when every scanning lane of
+// the wave qualifies (wave-uniform: one scan variant a wave); a lane of zero weights then starts from best = +inf,
+// which rejects every candidate as the test did (sumq2 = 0: inf * 0 is NaN). (IQ1_M keeps its single scan: the
+// same change measured slower there, its loop's register allocation being the cost.)
+template <bool B> struct ScanTest { static constexpr bool q2 = B; };
+template <int N> DEV bool iq1_weights_plain(const float (&w)[N], bool &any) {
+    bool ok = true;
+    any = false;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        ok = ok && (w[i] == 0.f || (w[i] >= 0x1p-100f && w[i] <= 0x1p100f));
+        any = any || w[i] > 0.f;
+    }
+    return ok;
+}
+
 // position of element i in the stable ascending order of x
 template <int N> DEV void stable_ranks(const float (&x)[N], Lv<N> &R) {
 #pragma unroll
@@ -127,6 +146,9 @@ struct KIQ1S : Iq8Tab<2048> {
         float scale = 0.f;
         int gi4[4] = {0, 0, 0, 0}, m4[4] = {0, 0, 0, 0};
         CoopWS &ws = *(CoopWS *)wave_ws<KIQ1S>(img);
+        bool wany;
+        const bool wplain = iq1_weights_plain<N>(weight, wany);
+        const bool q2pos = !__ballot(!(mx < EPS_IQ1S) && !wplain);     // (wave-uniform)
         if (!(mx < EPS_IQ1S)) {
             Lv<N> R;
             stable_ranks<N>(x, R);
@@ -148,33 +170,42 @@ struct KIQ1S : Iq8Tab<2048> {
                     totw = sumw[j] + tw;
                 }
             }
-            float best_score = -FLT_MAX;
             scale = mx;
-            int besti1 = -1, besti2 = -1, best_shift = 0;
-            for (int i1 = 0; i1 <= N; ++i1) {
-                const float s1x = i1 < N ? sumx[i1 & (N - 1)] : totx, s1w = i1 < N ? sumw[i1 & (N - 1)] : totw;
-                const float a_x = s1x - sumx[0], a_w = s1w - sumw[0];
-                for (int i2 = i1; i2 <= N; ++i2) {
-                    const float s2x = i2 < N ? sumx[i2 & (N - 1)] : totx, s2w = i2 < N ? sumw[i2 & (N - 1)] : totw;
-                    float sumqx = a_x * xp0 + (s2x - s1x) * xp1 + (totx - s2x) * xp2;
-                    float sumq2 = a_w * xp0 * xp0 + (s2w - s1w) * xp1 * xp1 + (totw - s2w) * xp2 * xp2;
-                    if ((sumq2 > 0) & (sumqx * sumqx > best_score * sumq2)) {    // (one branch, both tests)
-                        scale = sumqx / sumq2;
-                        best_score = scale * sumqx;
-                        besti1 = i1; besti2 = i2; best_shift = 1;
-                    }
-                    sumqx = a_x * xm0 + (s2x - s1x) * xm1 + (totx - s2x) * xm2;
-                    sumq2 = a_w * xm0 * xm0 + (s2w - s1w) * xm1 * xm1 + (totw - s2w) * xm2 * xm2;
-                    if ((sumq2 > 0) & (sumqx * sumqx > best_score * sumq2)) {
-                        scale = sumqx / sumq2;
-                        best_score = scale * sumqx;
-                        besti1 = i1; besti2 = i2; best_shift = -1;
+            int bidx = -1;            // the accepted candidate: i1 << 8 | i2 << 1 | (shift -1)
+            auto scan = [&](auto tst) {
+                constexpr bool TQ2 = decltype(tst)::q2;
+                float best_score = TQ2 || wany ? -FLT_MAX : __builtin_inff();
+                for (int i1 = 0; i1 <= N; ++i1) {
+                    const float s1x = i1 < N ? sumx[i1 & (N - 1)] : totx, s1w = i1 < N ? sumw[i1 & (N - 1)] : totw;
+                    const float a_x = s1x - sumx[0], a_w = s1w - sumw[0];
+                    for (int i2 = i1; i2 <= N; ++i2) {
+                        const float s2x = i2 < N ? sumx[i2 & (N - 1)] : totx;
+                        const float s2w = i2 < N ? sumw[i2 & (N - 1)] : totw;
+                        const int id = (i1 << 8) | (i2 << 1);
+                        float sumqx = a_x * xp0 + (s2x - s1x) * xp1 + (totx - s2x) * xp2;
+                        float sumq2 = a_w * xp0 * xp0 + (s2w - s1w) * xp1 * xp1 + (totw - s2w) * xp2 * xp2;
+                        if ((!TQ2 || sumq2 > 0) & (sumqx * sumqx > best_score * sumq2)) {   // (one branch, both tests)
+                            scale = sumqx / sumq2;
+                            best_score = scale * sumqx;
+                            bidx = id;
+                        }
+                        sumqx = a_x * xm0 + (s2x - s1x) * xm1 + (totx - s2x) * xm2;
+                        sumq2 = a_w * xm0 * xm0 + (s2w - s1w) * xm1 * xm1 + (totw - s2w) * xm2 * xm2;
+                        if ((!TQ2 || sumq2 > 0) & (sumqx * sumqx > best_score * sumq2)) {
+                            scale = sumqx / sumq2;
+                            best_score = scale * sumqx;
+                            bidx = id | 1;
+                        }
                     }
                 }
-            }
-            if (besti1 < 0 || besti2 < 0 || best_shift == 0) {
+            };
+            if (q2pos) scan(ScanTest<false>{});
+            else scan(ScanTest<true>{});
+            if (bidx < 0) {
                 scale = 0.f;
             } else {
+                const int besti1 = bidx >> 8, besti2 = (bidx >> 1) & 127;
+                int best_shift = bidx & 1 ? -1 : 1;
                 live = true;
                 const bool flip = scale < 0;
                 if (flip) { scale = -scale; best_shift = -best_shift; }
