@@ -6,8 +6,11 @@
 // cross-lane arithmetic reorders a sum; the few super-block-wide quantities are lane-to-lane chains (sums) or
 // order-free reductions (max). A wave therefore quantizes 64/G super-blocks at once, with 100% lane occupancy in the
 // fixed-trip-count search loops. Each wave assembles its super-blocks' output bytes in an LDS image and writes them
-// to HBM as one contiguous, dword-coalesced range. Workgroups of 4 waves loop over the super-blocks (grid-stride),
-// so the per-workgroup LDS table staging of the i-quants is paid once per workgroup.
+// to HBM as one contiguous, dword-coalesced range. For the types with neighbour searches (tiles of varying cost) the
+// launch holds as many workgroups as the CUs keep resident, and each wave takes its tiles (64/G super-blocks) one at
+// a time from a counter: the waves sweep the tensor once, in order (an expert's importance row is read while the
+// whole chip works on that expert), every wave busy until the counter runs past the end. The other types loop over
+// the tiles grid-stride. The per-workgroup LDS table staging of the i-quants is paid once per workgroup.
 #pragma once
 #include "common.cuh"
 
@@ -29,6 +32,10 @@ struct QParams {
     const int32_t *map3;
     int grid_size, map_size, neigh_len;
     int *err;               // set when a search finds no candidate (the reference traps there)
+    // the launch's tile counter (zeroed on the stream before the launch): after its first tile (its wave number) each
+    // wave takes the next from it (grid waves + the counter's old value), so the resident waves sweep the tensor once,
+    // in order, and finish together; nullptr: a fixed grid-stride order
+    unsigned long long *tiles;
     // strided views (the LDLQ loop quantizes one block column of every row): unit b reads its weights at element
     // b*sb_stride + sb_off, its importance at row*qw_stride + qw_off, and writes its block at byte
     // b*out_stride + out_off. The contiguous defaults are sb_stride = BS, qw_stride = BS, out_stride = BB, 0 offsets.
@@ -106,6 +113,14 @@ template <bool NT = false> DEV void img_store(uint8_t *dst, const uint8_t *img, 
     if (tail && lane == 0) *(uint16_t *)(dst + nbytes - 2) = *(const uint16_t *)(img + nbytes - 2);
 }
 
+// ------------------------------------------------------------------ the tile queue
+// lane 0's 64-bit value on every lane (wave-uniform)
+DEV int64_t wave_u64(unsigned long long v) {
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v);
+    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
+    return (int64_t)(((unsigned long long)hi << 32) | lo);
+}
+
 // ------------------------------------------------------------------ the kernel
 // T provides: BS (weights a unit: 256, or 32 for Q8_0 / IQ4_NL), G (lanes a unit), N (= BS / G), BB (unit bytes),
 // TAB (LDS table bytes, 0 for none),
@@ -121,6 +136,10 @@ template <class T> DEV uint8_t *wave_ws(uint8_t *img) { return img + img_bytes<T
 // share a CU's LDS: one workgroup of twice the waves shares one copy of the tables
 template <class T, class = void> struct wgw_of { static constexpr int v = WG_WAVES; };
 template <class T> struct wgw_of<T, decltype((void)T::WGW)> { static constexpr int v = T::WGW; };
+// QUEUE (optional): tiles from the launch's counter (types whose tiles vary in cost: the neighbour searches), one
+// resident grid; without it a grid-stride order over up to 32 waves a CU (tiles of equal cost)
+template <class T, class = void> struct queue_of { static constexpr bool v = false; };
+template <class T> struct queue_of<T, decltype((void)T::QUEUE)> { static constexpr bool v = T::QUEUE; };
 // WPE (optional): the waves per SIMD the register allocation must allow (default 2)
 template <class T, class = void> struct wpe_of { static constexpr int v = 2; };
 template <class T> struct wpe_of<T, decltype((void)T::WPE)> { static constexpr int v = T::WPE; };
@@ -138,7 +157,9 @@ __global__ __launch_bounds__(64 * wgw_of<T>::v) __attribute__((amdgpu_waves_per_
     const int g = lane % T::G, slot = lane / T::G;
     uint8_t *img = lds + T::TAB + wave * wave_bytes<T>();
     const int64_t nwaves = (int64_t)gridDim.x * WGW;
-    for (int64_t t = (int64_t)blockIdx.x * WGW + wave; t * SPW < p.nsb; t += nwaves) {
+    const bool queue = queue_of<T>::v && p.tiles != nullptr;       // (compile-time false for the other types)
+    int64_t t = (int64_t)blockIdx.x * WGW + wave;        // (the first tiles in wave order: no burst on the counter)
+    while (t * SPW < p.nsb) {
         const int64_t b0 = t * SPW;
         const int nact = (int)(p.nsb - b0 < SPW ? p.nsb - b0 : SPW);
         const int64_t b = b0 + (slot < nact ? slot : nact - 1);
@@ -146,6 +167,9 @@ __global__ __launch_bounds__(64 * wgw_of<T>::v) __attribute__((amdgpu_waves_per_
         wave_sync();
         float x[T::N];
         SrcLoad<SRC, T::N>::load(p.src, b * p.sb_stride + p.sb_off + g * T::N, x);
+        // the next tile, asked for now (lane 0's atomic returns while this tile is quantized)
+        unsigned long long tn = 0;
+        if (queue && lane == 0) tn = atomicAdd(p.tiles, 1ull);
         const float *qw = p.qw ? p.qw + qw_row(p, b) * p.qw_stride + p.qw_off + g * T::N : nullptr;
         T::quant(x, qw, g, img, slot * T::BB, lds, p);
         wave_sync();
@@ -157,5 +181,6 @@ __global__ __launch_bounds__(64 * wgw_of<T>::v) __attribute__((amdgpu_waves_per_
             for (int h = g; h < T::BB / 2; h += T::G) o[h] = s[h];
         }
         wave_sync();
+        t = queue ? nwaves + wave_u64(tn) : t + nwaves;
     }
 }

@@ -13,6 +13,7 @@
 #include <cstring>
 #include <algorithm>
 #include <cstdlib>
+#include <atomic>
 #include <mutex>
 #include <thread>
 #include <unordered_map>
@@ -37,9 +38,21 @@ extern "C" size_t gpuq_block_bytes(int type);
 static constexpr int64_t LDLQ_SCRATCH_ROWS = 8192;
 static __device__ __align__(256) double scratch[2 * LDLQ_SCRATCH_ROWS * 256];
 
+// The quantize launches' tile counters (the tile queue of k_quant): each launch takes the next of TILE_SLOTS slots
+// and zeroes it on its stream before the kernel, so launches in flight at once on any streams use distinct counters
+// while there are at most TILE_SLOTS of them. Addresses taken per device at gpuq_init, as for `scratch`.
+static constexpr unsigned TILE_SLOTS = 256;
+static __device__ __align__(256) unsigned long long tile_ctr[TILE_SLOTS];
+
+__global__ void k_tile_reset(unsigned long long *ctr) {
+    if (threadIdx.x == 0) *ctr = 0ull;
+}
+
 namespace {
 
 double *g_scratch[64] = {};    // per device: the device address of `scratch`
+unsigned long long *g_tile_ctr[64] = {};   // per device: the device address of `tile_ctr`
+std::atomic<unsigned> g_tile_slot{0};
 
 struct Tabs {
     bool ok = false;
@@ -184,15 +197,33 @@ template <class V> bool upload(V **dst, const std::vector<V> &src) {
 }
 
 // ------------------------------------------------------------------ launch plumbing
-template <class T, int SRC> bool launch_q(const QParams &p, hipStream_t st) {
+// the launch. Queue types: as many workgroups as the CUs hold at once (the kernel's occupancy, queried once), each
+// wave taking tiles from a zeroed counter until they run out. Others: up to 32 waves a CU in flight or queued,
+// grid-stride.
+template <class T, int SRC> bool launch_q(const QParams &p0, hipStream_t st) {
     constexpr int spw = 64 / T::G, wgw = wgw_of<T>::v;
-    const int64_t tiles = (p.nsb + spw - 1) / spw;
-    int64_t wgs = (tiles + wgw - 1) / wgw;
-    const int64_t cap = (int64_t)g_ncu * 32 / wgw;          // 32 waves a CU in flight or queued
-    if (wgs > cap) wgs = cap;
-    if (wgs < 1) wgs = 1;
     static_assert((size_t)T::TAB + wgw * wave_bytes<T>() <= 160 * 1024, "a workgroup's LDS within a CU's 160 KiB");
     const size_t lds = (size_t)T::TAB + wgw * wave_bytes<T>();
+    const int64_t tiles = (p0.nsb + spw - 1) / spw;
+    int64_t wgs = (tiles + wgw - 1) / wgw;
+    int64_t cap = (int64_t)g_ncu * 32 / wgw;
+    QParams p = p0;
+    p.tiles = nullptr;
+    if (queue_of<T>::v && g_device >= 0 && g_device < 64 && g_tile_ctr[g_device]) {
+        static std::atomic<int> occ{0};
+        int n = occ.load();
+        if (n == 0) {
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_quant<T, SRC>, 64 * wgw, lds) != hipSuccess ||
+                n < 1)
+                return false;
+            occ.store(n);
+        }
+        cap = (int64_t)g_ncu * n;
+        p.tiles = g_tile_ctr[g_device] + g_tile_slot.fetch_add(1) % TILE_SLOTS;
+    }
+    if (wgs > cap) wgs = cap;
+    if (wgs < 1) wgs = 1;
+    if (p.tiles) hipLaunchKernelGGL(k_tile_reset, dim3(1), dim3(64), 0, st, p.tiles);
     hipLaunchKernelGGL((k_quant<T, SRC>), dim3((unsigned)wgs), dim3(64 * wgw), lds, st, p);
     return hipGetLastError() == hipSuccess;
 }
@@ -561,6 +592,9 @@ extern "C" int gpuq_init(const char *tables, int device) {
         void *ptr = nullptr;
         if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return 4;
         g_scratch[device] = (double *)ptr;
+        ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(tile_ctr)) != hipSuccess || !ptr) return 4;
+        g_tile_ctr[device] = (unsigned long long *)ptr;
     }
     int ncu = 0;
     if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && ncu > 0) g_ncu = ncu;

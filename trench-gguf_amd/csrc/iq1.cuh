@@ -126,6 +126,7 @@ template <int G, int N> DEV void grp_chain_sum2(const float (&a)[N], const float
 // block: d qs[32] qh[8] u16 (50 bytes); lane g = 32-weight block g
 struct KIQ1S : Iq8Tab<2048> {
     static constexpr int BS = QK, G = 8, N = 32, BB = 50, WS = COOP_WS_BYTES;
+    static constexpr bool QUEUE = true;         // (tiles of varying cost: the tile queue)
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
                           const QParams &p) {
         const uint64_t *grid = Iq8Tab<2048>::grid(lds);
@@ -277,6 +278,7 @@ struct KIQ1S : Iq8Tab<2048> {
 // block: qs[32] qh[16] scales[8] (56 bytes); lane g = 16-weight block g
 struct KIQ1M : Iq8Tab<2048> {
     static constexpr int BS = QK, G = 16, N = 16, BB = 56, WS = COOP_WS_BYTES;
+    static constexpr bool QUEUE = true;         // (tiles of varying cost: the tile queue)
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
                           const QParams &p) {
         const uint64_t *grid = Iq8Tab<2048>::grid(lds);

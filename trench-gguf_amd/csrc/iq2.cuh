@@ -243,6 +243,7 @@ DEV void window_group(const float (&xk)[8], const float (&waux)[8], const float 
 // block: d qs[32] u16 (66 bytes); lane g = 32-weight sub-block g; q2[2g] at 2+8g, q2[2g+1] at 6+8g
 struct KIQ2XXS : Iq8Tab<256> {
     static constexpr int BS = QK, G = 8, N = 32, BB = 66, NTRIAL = 13;
+    static constexpr bool QUEUE = true;         // (tiles of varying cost: the tile queue)
     static constexpr int TW = 7;        // trials a window: windows 0..6 and 7..12
     // per-wave LDS: the search workspace, shared by the filtered, the 4-list and the single-list searches and their
     // staged values; eight waves a workgroup share one copy of the tables (the workspace would not let two four-wave
@@ -618,6 +619,7 @@ DEV float iq2_16_search(const float (&x)[16], const float (&qv)[16], float sigma
 // IQ2_S: block d qs[64] (32 grid bytes, 32 sign bytes) qh[8] scales[8] (82 bytes); lane g = 16-weight sub-block g
 struct KIQ2S : Iq8Tab<1024> {
     static constexpr int BS = QK, G = 16, N = 16, BB = 82, WS = coop_wsm_bytes<4, 16, true, 2>(), WGW = 8;
+    static constexpr bool QUEUE = true;         // (tiles of varying cost: the tile queue)
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
                           const QParams &p) {
         float qv[N], sq[N];
@@ -652,6 +654,7 @@ struct KIQ2S : Iq8Tab<1024> {
 // IQ2_XS: block d qs[32] u16 scales[8] (74 bytes); qs[2g+k] = grid index | signs << 9
 struct KIQ2XS : Iq8Tab<512> {
     static constexpr int WS0 = coop_wsm_bytes<4, 16, true, 2>();
+    static constexpr bool QUEUE = true;         // (tiles of varying cost: the tile queue)
     static constexpr int BS = QK, G = 16, N = 16, BB = 74, WGW = 8,
                          WS = (((int)sizeof(FiltWS<IQ2XS_TW>) > WS0 ? (int)sizeof(FiltWS<IQ2XS_TW>) : WS0) + 15) & ~15;
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,

@@ -190,6 +190,7 @@ DEV float iq3_search(const float (&x)[32], const float (&qv)[32], float sigma2, 
 // IQ3_XXS: block d qs[96] = 64 grid bytes, then 8 u32 signs-and-scales (98 bytes)
 struct KIQ3XXS : Iq4Tab<256> {
     static constexpr int BS = QK, G = 8, N = 32, BB = 98, WS = coop_wsm_bytes<4, 8, true>();
+    static constexpr bool QUEUE = true;         // (tiles of varying cost: the tile queue)
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
                           const QParams &p) {
         const int32_t *map = Iq4Tab<256>::map(lds);
@@ -229,6 +230,7 @@ struct KIQ3XXS : Iq4Tab<256> {
 // qs / signs cursors (ggml's quirk, kept by the reference): the next live sub-block takes its slot.
 struct KIQ3S : Iq4Tab<512> {
     static constexpr int BS = QK, G = 8, N = 32, BB = 110, WS = coop_wsm_bytes<4, 8, true>();
+    static constexpr bool QUEUE = true;         // (tiles of varying cost: the tile queue)
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
                           const QParams &p) {
         const int32_t *map = Iq4Tab<512>::map(lds);
