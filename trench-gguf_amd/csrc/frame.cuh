@@ -32,9 +32,9 @@ struct QParams {
     const int32_t *map3;
     int grid_size, map_size, neigh_len;
     int *err;               // set when a search finds no candidate (the reference traps there)
-    // the launch's tile counter (zeroed on the stream before the launch): after its first tile (its wave number) each
-    // wave takes the next from it (grid waves + the counter's old value), so the resident waves sweep the tensor once,
-    // in order, and finish together; nullptr: a fixed grid-stride order
+    // the launch's tile counter (zeroed on the stream before the launch): after its first chunk of tiles (its wave
+    // number) each wave takes the next from it (grid waves + the counter's old value), so the resident waves sweep
+    // the tensor once, in order, and finish together; nullptr: a fixed grid-stride order
     unsigned long long *tiles;
     // strided views (the LDLQ loop quantizes one block column of every row): unit b reads its weights at element
     // b*sb_stride + sb_off, its importance at row*qw_stride + qw_off, and writes its block at byte
@@ -158,7 +158,14 @@ __global__ __launch_bounds__(64 * wgw_of<T>::v) __attribute__((amdgpu_waves_per_
     uint8_t *img = lds + T::TAB + wave * wave_bytes<T>();
     const int64_t nwaves = (int64_t)gridDim.x * WGW;
     const bool queue = queue_of<T>::v && p.tiles != nullptr;       // (compile-time false for the other types)
-    int64_t t = (int64_t)blockIdx.x * WGW + wave;        // (the first tiles in wave order: no burst on the counter)
+    // queued tiles come in chunks of KT whose source bytes start and end on 128-byte lines (the 17-byte MXFP4 and
+    // 34-byte Q8_0 blocks), so that no line is fetched by two waves of different XCDs
+    constexpr int KT = !queue_of<T>::v ? 1 : SRC == T_MXFP4 ? (SPW >= 16 ? 1 : 16 / SPW)
+                                           : SRC == T_Q8_0 ? (SPW >= 8 ? 1 : 8 / SPW) : 1;
+    int64_t c = (int64_t)blockIdx.x * WGW + wave;        // (the first chunks in wave order: no burst on the counter)
+    int k = 0;                                           // the tile in the chunk
+    int64_t t = c * KT;
+    unsigned long long tn = 0;
     while (t * SPW < p.nsb) {
         const int64_t b0 = t * SPW;
         const int nact = (int)(p.nsb - b0 < SPW ? p.nsb - b0 : SPW);
@@ -167,9 +174,8 @@ __global__ __launch_bounds__(64 * wgw_of<T>::v) __attribute__((amdgpu_waves_per_
         wave_sync();
         float x[T::N];
         SrcLoad<SRC, T::N>::load(p.src, b * p.sb_stride + p.sb_off + g * T::N, x);
-        // the next tile, asked for now (lane 0's atomic returns while this tile is quantized)
-        unsigned long long tn = 0;
-        if (queue && lane == 0) tn = atomicAdd(p.tiles, 1ull);
+        // the next chunk, asked for at a chunk's first tile (lane 0's atomic returns while the chunk is quantized)
+        if (queue && k == 0 && lane == 0) tn = atomicAdd(p.tiles, 1ull);
         const float *qw = p.qw ? p.qw + qw_row(p, b) * p.qw_stride + p.qw_off + g * T::N : nullptr;
         T::quant(x, qw, g, img, slot * T::BB, lds, p);
         wave_sync();
@@ -181,6 +187,10 @@ __global__ __launch_bounds__(64 * wgw_of<T>::v) __attribute__((amdgpu_waves_per_
             for (int h = g; h < T::BB / 2; h += T::G) o[h] = s[h];
         }
         wave_sync();
-        t = queue ? nwaves + wave_u64(tn) : t + nwaves;
+        if (++k == KT) {
+            c = queue ? nwaves + wave_u64(tn) : c + nwaves;
+            k = 0;
+        }
+        t = c * KT + k;
     }
 }
