@@ -81,6 +81,31 @@ DEV int div_small(int a, int b) {
     return q;
 }
 
+// The deal's mark table: walker L's first piece is L*R; this lane's lists hold pieces [s0, s0 + sum np) of the wave's
+// concatenation, list m the np[m] pieces after those of lists 0..m-1. For each walker whose first piece falls in them
+// (at most a few: the lane's pieces over R), mark[L] = (m*64 + lane) | (the piece's number in list m << SH).
+template <int M, int SH> DEV void deal_marks(int *mark, const int (&np)[M], int s0, int R) {
+    const int lane = lane_id();
+    int tot = 0;
+#pragma unroll
+    for (int m = 0; m < M; ++m) tot += np[m];
+    const int lf = div_small(s0 + R - 1, R);
+    const int ll = div_small(s0 + tot - 1, R);           // (no pieces: ll < lf)
+    for (int L = lf; L <= ll && L < 64; ++L) {
+        int j = (int)__umul24((unsigned)L, (unsigned)R) - s0;   // the walker's first piece among the lane's
+        int m = M - 1;
+        bool found = false;
+#pragma unroll
+        for (int i = 0; i < M; ++i) {                    // the list holding it (lists of no pieces skipped)
+            const bool hit = !found && j < np[i];
+            m = hit ? i : m;
+            j = found || hit ? j : j - np[i];
+            found = found || hit;
+        }
+        mark[L] = (m * 64 + lane) | (j << SH);
+    }
+}
+
 // inclusive prefix sum over the wave's 64 lanes (DPP: shifts within rows of 16, then the row broadcasts)
 DEV int wave_incl_scan(int v) {
     v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);     // row_shr:1
@@ -160,17 +185,10 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
     }
     const int R = (total + 63) >> 6;                    // pieces a walker
     {
-        int start = incl - tot;                         // the list's first piece
+        int np[M];
 #pragma unroll
-        for (int m = 0; m < M; ++m) {
-            // walkers L with start <= L*R < start + np begin in list m (none when np == 0: lf > ll)
-            const int np = (cnt[m] + CH - 1) >> CSH;
-            const int lf = div_small(start + R - 1, R);
-            const int ll = div_small(start + np - 1, R);
-            for (int L = lf; L <= ll && L < 64; ++L)
-                ws.mark[L] = (m * 64 + lane) | (((int)__umul24((unsigned)L, (unsigned)R) - start) << 8);
-            start += np;
-        }
+        for (int m = 0; m < M; ++m) np[m] = (cnt[m] + CH - 1) >> CSH;
+        deal_marks<M, 8>(ws.mark, np, incl - tot, R);
     }
     wave_sync();
     const int p0 = (int)__umul24((unsigned)lane, (unsigned)R);   // this walker's first piece

@@ -125,17 +125,10 @@ DEV void coop_filter(const int (&cnt)[W], const int (&off)[W], const int (&ntr)[
     }
     const int R = (total + 63) >> 6;                    // pieces a walker
     {
-        int start = incl - tot;                         // the list's first piece
+        int np[W];
 #pragma unroll
-        for (int m = 0; m < W; ++m) {
-            // walkers L with start <= L*R < start + np begin in list m (none when np == 0: lf > ll)
-            const int np = (cnt[m] + CH - 1) >> CSH;
-            const int lf = div_small(start + R - 1, R);
-            const int ll = div_small(start + np - 1, R);
-            for (int L = lf; L <= ll && L < 64; ++L)
-                ws.mark[L] = (m * 64 + lane) | (((int)__umul24((unsigned)L, (unsigned)R) - start) << 9);
-            start += np;
-        }
+        for (int m = 0; m < W; ++m) np[m] = (cnt[m] + CH - 1) >> CSH;
+        deal_marks<W, 9>(ws.mark, np, incl - tot, R);
     }
     wave_sync();
     const int p0 = (int)__umul24((unsigned)lane, (unsigned)R);   // this walker's first piece
