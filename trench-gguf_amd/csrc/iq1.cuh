@@ -48,28 +48,43 @@ struct EvalIq1 {
     }
 };
 
-// Group k's grid point on every lane of the wave (all lanes call it together; k, live as the caller has them): a key
-// on the grid directly, else the cooperative search over its list. Returns 0 for a lane that is not live, and flags
-// a search that accepts nothing.
-DEV int iq1_group_point(bool live, int m, const float *xk, const float *wk, float scale, bool minus,
-                        const QParams &p, const uint64_t *grid, CoopWS &ws, bool &on_grid) {
-    const bool srch = live && m < 0;
-    on_grid = !srch;
-    const int cnt = srch ? m3_cnt(m) : 0, off = srch ? m3_off(m) : 0;
-    if (srch) coop_stage<8>(ws, xk, wk);
+// Two groups' grid points on every lane of the wave (all lanes call it together; live as the caller has it): a key
+// on the grid directly, else the cooperative search over its list, both groups' lists in one wave-wide call (two
+// lists a lane, each with its group's staged values, row k*64 + lane). gi[k] is 0 for a lane that is not live; a
+// search that accepts nothing is flagged and yields 0. og[k]: no search was needed.
+using Iq1WS = CoopWSM<2, 16, true>;
+DEV void iq1_group_points2(bool live, const int (&m)[2], const float *x0, const float *w0, const float *x1,
+                           const float *w1, float scale, const bool (&minus)[2], const QParams &p,
+                           const uint64_t *grid, Iq1WS &ws, int (&gi)[2], bool (&og)[2]) {
+    int cnt[2], off[2], g[2];
+    float ssc[2];
     bool neg = false;                   // (a negative importance: distances of any sign, see coop.cuh)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) neg = neg || wk[i] < 0.f;
-    const float ssc = minus ? -scale : scale;
-    const int gi = __ballot(srch && neg) ? coop_search<4, true>(cnt, off, ssc, p.neigh, p.neigh_len, ws, EvalIq1{grid})
-                                         : coop_search(cnt, off, ssc, p.neigh, p.neigh_len, ws, EvalIq1{grid});
-    if (!live) return 0;
-    if (!srch) return m;
-    if (gi < 0) {
-        flag_err(p);
-        return 0;
+    for (int k = 0; k < 2; ++k) {
+        const float *xk = k ? x1 : x0, *wk = k ? w1 : w0;
+        const bool srch = live && m[k] < 0;
+        og[k] = !srch;
+        cnt[k] = srch ? m3_cnt(m[k]) : 0;
+        off[k] = srch ? m3_off(m[k]) : 0;
+        ssc[k] = minus[k] ? -scale : scale;
+        if (srch) coop_stage<8>(ws, xk, wk, k * 64 + lane_id());
+#pragma unroll
+        for (int i = 0; i < 8; ++i) neg = neg || (srch && wk[i] < 0.f);
     }
-    return gi;
+    if (__ballot(neg)) coop_search_m<2, 4, true>(cnt, off, ssc, p.neigh, p.neigh_len, ws, EvalIq1{grid}, g);
+    else coop_search_m<2, 4, false>(cnt, off, ssc, p.neigh, p.neigh_len, ws, EvalIq1{grid}, g);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        gi[k] = 0;
+        if (!live) continue;
+        if (og[k]) {
+            gi[k] = m[k];
+        } else if (g[k] < 0) {
+            flag_err(p);
+        } else {
+            gi[k] = g[k];
+        }
+    }
 }
 
 // Whether IQ1_S's partition scan may drop its `sumq2 > 0` test: a candidate's sumq2 is
@@ -125,7 +140,7 @@ template <int G, int N> DEV void grp_chain_sum2(const float (&a)[N], const float
 // ------------------------------------------------------------------ IQ1_S (gpuq/gpuq.hip:389-514)
 // block: d qs[32] qh[8] u16 (50 bytes); lane g = 32-weight block g
 struct KIQ1S : Iq8Tab<2048> {
-    static constexpr int BS = QK, G = 8, N = 32, BB = 50, WS = COOP_WS_BYTES;
+    static constexpr int BS = QK, G = 8, N = 32, BB = 50, WS = coop_wsm_bytes<2, 16, true>(), WGW = 8;
     static constexpr bool QUEUE = true;         // (tiles of varying cost: the tile queue)
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
                           const QParams &p) {
@@ -146,7 +161,7 @@ struct KIQ1S : Iq8Tab<2048> {
         bool live = false, minus = false;
         float scale = 0.f;
         int gi4[4] = {0, 0, 0, 0}, m4[4] = {0, 0, 0, 0};
-        CoopWS &ws = *(CoopWS *)wave_ws<KIQ1S>(img);
+        Iq1WS &ws = *(Iq1WS *)wave_ws<KIQ1S>(img);
         bool wany;
         const bool wplain = iq1_weights_plain<N>(weight, wany);
         const bool q2pos = !__ballot(!(mx < EPS_IQ1S) && !wplain);     // (wave-uniform)
@@ -226,13 +241,19 @@ struct KIQ1S : Iq8Tab<2048> {
                 }
             }
         }
-        // the groups' points (every lane: the neighbour search is wave-wide)
+        // the groups' points (every lane: the neighbour search is wave-wide), two groups a call
         bool all_on_grid = true;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            bool og;
-            gi4[k] = iq1_group_point(live, m4[k], x + 8 * k, weight + 8 * k, scale, minus, p, grid, ws, og);
-            all_on_grid = all_on_grid && og;
+        for (int h = 0; h < 2; ++h) {
+            const int mk[2] = {m4[2 * h], m4[2 * h + 1]};
+            const bool mn[2] = {minus, minus};
+            int gi[2];
+            bool og[2];
+            iq1_group_points2(live, mk, x + 16 * h, weight + 16 * h, x + 16 * h + 8, weight + 16 * h + 8, scale, mn, p,
+                              grid, ws, gi, og);
+            gi4[2 * h] = gi[0];
+            gi4[2 * h + 1] = gi[1];
+            all_on_grid = all_on_grid && og[0] && og[1];
         }
         if (live) {
             {
@@ -277,7 +298,7 @@ struct KIQ1S : Iq8Tab<2048> {
 // ------------------------------------------------------------------ IQ1_M (gpuq/gpuq.hip:516-688)
 // block: qs[32] qh[16] scales[8] (56 bytes); lane g = 16-weight block g
 struct KIQ1M : Iq8Tab<2048> {
-    static constexpr int BS = QK, G = 16, N = 16, BB = 56, WS = COOP_WS_BYTES;
+    static constexpr int BS = QK, G = 16, N = 16, BB = 56, WS = coop_wsm_bytes<2, 16, true>(), WGW = 8;
     static constexpr bool QUEUE = true;         // (tiles of varying cost: the tile queue)
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
                           const QParams &p) {
@@ -299,7 +320,7 @@ struct KIQ1M : Iq8Tab<2048> {
         int best_k = 0;       // the shift combination (0 for a skipped block, masks[0] = 0)
         float scale = 0.f;
         int gi2[2] = {0, 0}, mk2[2] = {0, 0};
-        CoopWS &ws = *(CoopWS *)wave_ws<KIQ1M>(img);
+        Iq1WS &ws = *(Iq1WS *)wave_ws<KIQ1M>(img);
         if (!(mx < EPS_IQ1M)) {
             Lv<N> R;
             stable_ranks<N>(x, R);
@@ -389,14 +410,13 @@ struct KIQ1M : Iq8Tab<2048> {
                 }
             }
         }
-        // the groups' points (every lane: the neighbour search is wave-wide)
-        bool all_on_grid = true;
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const bool minus = k == 0 ? !(best_k < 2) : !(best_k % 2 == 0);
-            bool og;
-            gi2[k] = iq1_group_point(live, mk2[k], x + 8 * k, weight + 8 * k, scale, minus, p, grid, ws, og);
-            all_on_grid = all_on_grid && og;
+        // the groups' points (every lane: the neighbour search is wave-wide), both groups in one call
+        bool all_on_grid;
+        {
+            const bool mn[2] = {!(best_k < 2), !(best_k % 2 == 0)};
+            bool og[2];
+            iq1_group_points2(live, mk2, x, weight, x + 8, weight + 8, scale, mn, p, grid, ws, gi2, og);
+            all_on_grid = og[0] && og[1];
         }
         if (live) {
             {
