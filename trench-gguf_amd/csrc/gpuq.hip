@@ -41,7 +41,7 @@ static __device__ __align__(256) double scratch[2 * LDLQ_SCRATCH_ROWS * 256];
 // The quantize launches' tile counters (the tile queue of k_quant): each launch takes the next of TILE_SLOTS slots
 // and zeroes it on its stream before the kernel, so launches in flight at once on any streams use distinct counters
 // while there are at most TILE_SLOTS of them. Addresses taken per device at gpuq_init, as for `scratch`.
-static constexpr unsigned TILE_SLOTS = 256;
+static constexpr unsigned TILE_SLOTS = 4096;
 static __device__ __align__(256) unsigned long long tile_ctr[TILE_SLOTS];
 
 __global__ void k_tile_reset(unsigned long long *ctr) {
