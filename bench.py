@@ -338,6 +338,29 @@ def time_gpu(torch, gq, gpuq, wl, typ, steps, warmup):
     return ms, result
 
 
+def copy_reference(torch, total_bytes, steps=20):
+    """GB/s of a torch device copy that moves `total_bytes` (half read, half written), timed as time_gpu times a
+    kernel (HIP events, sources rotated past the Infinity Cache): what a plain streaming kernel of that size reaches"""
+    half = int(total_bytes // 2)
+    copies = int(2 * MALL_BYTES // half) + 1
+    srcs = [torch.empty(half, dtype=torch.uint8, device="cuda").fill_(1) for _ in range(copies)]
+    dsts = [torch.empty(half, dtype=torch.uint8, device="cuda") for _ in range(min(copies, 4))]
+    for i in range(3):
+        dsts[i % len(dsts)].copy_(srcs[i % copies])
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    hold_gpu(torch, 2.0 + 0.05 * steps)
+    e0.record(stream)
+    for i in range(steps):
+        dsts[i % len(dsts)].copy_(srcs[i % copies])
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    del srcs, dsts
+    return 2 * half / (ms / 1e3) / 1e9
+
+
 def host_api(torch, gq, gpuq, wl, typ, nmat, dev_out, reps=3):
     """PCIe-inclusive rate of the host entry point gpuq_requantize_batch on the first `nmat` matrices of the workload:
     source bytes in pageable host memory, blocks back into host memory (copies overlapped with the kernels); its bytes
@@ -413,9 +436,12 @@ def cpu_and_roofline(torch, gq, gpuq, orc, orc_ops, wl, typ, ms, out_dev, sample
     if typ == gpuq.Q8_0:
         bpw = {0: 4.0, 30: 2.0}.get(wl.src, 17 / 32) + 34 / 32
         achieved = bpw * wl.n / (ms / 1e3) / 1e9
+        copy_gbs = copy_reference(torch, bpw * wl.n)
         entry["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                              "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                             "algorithmic_bytes_per_weight": bpw, "algorithmic_bytes": round(bpw * wl.n)}
+                             "algorithmic_bytes_per_weight": bpw, "algorithmic_bytes": round(bpw * wl.n),
+                             "device_copy_same_bytes_GBps": round(copy_gbs, 1),
+                             "frac_of_device_copy": round(achieved / copy_gbs, 4)}
     else:
         ops_rows = min(sample_rows, 64)
         sub = raw[: (ops_rows * wl.ncol) * {0: 4, 30: 2}.get(wl.src, 0)] if wl.src in (0, 30) else \
