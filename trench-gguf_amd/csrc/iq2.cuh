@@ -69,33 +69,37 @@ struct EvalIq8 {
     }
 };
 
-// The group's grid point on every lane of the wave (all lanes call it together): an active lane whose key is on the
-// grid takes that point (og = true), the others search their neighbour lists together (coop_search) with the values
-// the caller staged (coop_stage). Inactive lanes get 0. A search that accepts nothing flags the error (the reference
-// traps) and yields 0.
-template <int CH = 4>
-DEV int group_point_s(bool active, int k3, const int32_t *map3, const QParams &p, const uint64_t *grid, float scale,
-                      CoopWS &ws, bool &og) {
-    const int m = active ? map3[k3] : 0;
-    og = m >= 0;
-    const bool srch = active && m < 0;
-    const int off = srch ? m3_off(m) : 0;
-    const int cnt = srch ? m3_cnt(m) : 0;
-    const int gi = coop_search<CH>(cnt, off, scale, p.neigh, p.neigh_len, ws, EvalIq8{grid});
-    if (!srch) return active ? m : 0;
-    if (gi < 0) {
-        flag_err(p);
-        return 0;
+// Two groups' grid points on every lane of the wave (all lanes call it together), in one wave-wide search call: two
+// lists a lane, each with its group's x's and weights staged in row k*64 + lane. An active lane whose key is on the
+// grid takes that point (og), an active off-grid key the winner of its neighbour list, an inactive lane 0; a search
+// that accepts nothing flags the error (the reference traps) and yields 0.
+using Iq8WS2 = CoopWSM<2, 16, true>;
+DEV void group_points2_w(bool active, const int (&k3)[2], const int32_t *map3, const QParams &p, const uint64_t *grid,
+                         const float *x0, const float *w0, const float *x1, const float *w1, float scale, Iq8WS2 &ws,
+                         int (&gi)[2], bool (&og)[2]) {
+    int m[2], cnt[2], off[2], g[2];
+    const float sc[2] = {scale, scale};
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        m[k] = active ? map3[k3[k]] : 0;
+        og[k] = m[k] >= 0;
+        const bool srch = active && m[k] < 0;
+        off[k] = srch ? m3_off(m[k]) : 0;
+        cnt[k] = srch ? m3_cnt(m[k]) : 0;
+        coop_stage<8>(ws, k ? x1 : x0, k ? w1 : w0, k * 64 + lane_id());
     }
-    return gi;
-}
-
-// the same, staging the group's values (x's xv, weights wa) first
-template <int CH = 4>
-DEV int group_point_w(bool active, int k3, const int32_t *map3, const QParams &p, const uint64_t *grid,
-                      const float *xv, const float *wa, float scale, CoopWS &ws, bool &og) {
-    coop_stage<8>(ws, xv, wa);
-    return group_point_s<CH>(active, k3, map3, p, grid, scale, ws, og);
+    coop_search_m<2, 4>(cnt, off, sc, p.neigh, p.neigh_len, ws, EvalIq8{grid}, g);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        if (!(active && m[k] < 0)) {
+            gi[k] = active ? m[k] : 0;
+        } else if (g[k] < 0) {
+            flag_err(p);
+            gi[k] = 0;
+        } else {
+            gi[k] = g[k];
+        }
+    }
 }
 
 // signs of 8 values with even parity: an odd count flips the weight with the least w*x^2 (gpuq/gpuq.hip:272-289)
@@ -245,10 +249,11 @@ struct KIQ2XXS : Iq8Tab<256> {
     static constexpr int BS = QK, G = 8, N = 32, BB = 66, NTRIAL = 13;
     static constexpr bool QUEUE = true;         // (tiles of varying cost: the tile queue)
     static constexpr int TW = 7;        // trials a window: windows 0..6 and 7..12
-    // per-wave LDS: the search workspace, shared by the filtered, the 4-list and the single-list searches and their
-    // staged values; eight waves a workgroup share one copy of the tables (the workspace would not let two four-wave
+    // per-wave LDS: the search workspace, shared by the filtered, the 4-list, the 2-list and the 1-list searches and
+    // their staged values; eight waves a workgroup share one copy of the tables (the workspace would not let two four-wave
     // workgroups share a CU's LDS)
-    static constexpr int WS0 = coop_wsm_bytes<4>() > COOP_WS_BYTES ? coop_wsm_bytes<4>() : COOP_WS_BYTES;
+    static constexpr int WS1 = coop_wsm_bytes<4>() > COOP_WS_BYTES ? coop_wsm_bytes<4>() : COOP_WS_BYTES;
+    static constexpr int WS0 = coop_wsm_bytes<2, 16, true>() > WS1 ? coop_wsm_bytes<2, 16, true>() : WS1;
     static constexpr int WS = (((int)sizeof(FiltWS<TW>) > WS0 ? (int)sizeof(FiltWS<TW>) : WS0) + 15) & ~15;
     static constexpr int WGW = 8;
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
@@ -257,6 +262,7 @@ struct KIQ2XXS : Iq8Tab<256> {
         const int32_t *map3 = Iq8Tab<256>::map3(lds);
         CoopWS &ws = *(CoopWS *)wave_ws<KIQ2XXS>(img);
         CoopWSM<4> &wsm = *(CoopWSM<4> *)wave_ws<KIQ2XXS>(img);
+        Iq8WS2 &ws2 = *(Iq8WS2 *)wave_ws<KIQ2XXS>(img);
         FiltWS<TW> &fws = *(FiltWS<TW> *)wave_ws<KIQ2XXS>(img);
         float weight[N], xval[N];
         uint32_t bsg = 0;       // the 4 groups' 7-bit sign fields
@@ -347,15 +353,23 @@ struct KIQ2XXS : Iq8Tab<256> {
             uint32_t Pf = 0;
             float sumqx = 0, sumq2 = 0;
 #pragma unroll 1
-            for (int k = 0; k < 4; ++k) {
-                float waux[8];
+            for (int h = 0; h < 2; ++h) {       // groups 2h and 2h+1 in one search call
+                float wa0[8], wa1[8];
 #pragma unroll
-                for (int i = 0; i < 8; ++i) waux[i] = sqrtf(weight[i]);
-                bool og;
-                const int gi = group_point_w(fin || alt, group_key3(xval, id), map3, p, grid, xval, waux, fsc, ws, og);
-                Pf |= (uint32_t)gi << (8 * k);
-                sums_q8(weight, xval, grid[gi], sumqx, sumq2);
+                for (int i = 0; i < 8; ++i) {
+                    wa0[i] = sqrtf(weight[i]);
+                    wa1[i] = sqrtf(weight[8 + i]);
+                }
+                const int k3[2] = {group_key3(xval, id), group_key3(xval + 8, id)};
+                int gi[2];
+                bool og[2];
+                group_points2_w(fin || alt, k3, map3, p, grid, xval, wa0, xval + 8, wa1, fsc, ws2, gi, og);
+                Pf |= ((uint32_t)gi[0] | ((uint32_t)gi[1] << 8)) << (16 * h);
+                sums_q8(weight, xval, grid[gi[0]], sumqx, sumq2);
+                sums_q8(weight + 8, xval + 8, grid[gi[1]], sumqx, sumq2);
                 rot8(xval);
+                rot8(xval);
+                rot8(weight);
                 rot8(weight);
             }
             if (fin || alt) P = Pf;
