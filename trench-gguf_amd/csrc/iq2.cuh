@@ -250,8 +250,8 @@ struct KIQ2XXS : Iq8Tab<256> {
     static constexpr bool QUEUE = true;         // (tiles of varying cost: the tile queue)
     static constexpr int TW = 7;        // trials a window: windows 0..6 and 7..12
     // per-wave LDS: the search workspace, shared by the filtered, the 4-list, the 2-list and the 1-list searches and
-    // their staged values; eight waves a workgroup share one copy of the tables (the workspace would not let two four-wave
-    // workgroups share a CU's LDS)
+    // their staged values; eight waves a workgroup share one copy of the tables (the workspace would not let two
+    // four-wave workgroups share a CU's LDS)
     static constexpr int WS1 = coop_wsm_bytes<4>() > COOP_WS_BYTES ? coop_wsm_bytes<4>() : COOP_WS_BYTES;
     static constexpr int WS0 = coop_wsm_bytes<2, 16, true>() > WS1 ? coop_wsm_bytes<2, 16, true>() : WS1;
     static constexpr int WS = (((int)sizeof(FiltWS<TW>) > WS0 ? (int)sizeof(FiltWS<TW>) : WS0) + 15) & ~15;
