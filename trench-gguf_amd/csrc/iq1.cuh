@@ -53,6 +53,7 @@ struct EvalIq1 {
 // lists a lane, each with its group's staged values, row k*64 + lane). gi[k] is 0 for a lane that is not live; a
 // search that accepts nothing is flagged and yields 0. og[k]: no search was needed.
 using Iq1WS = CoopWSM<2, 16, true>;
+static_assert(sizeof(Iq1WS) >= 17 * 64 * sizeof(float2), "the rank-order slots fit the search workspace");
 DEV void iq1_group_points2(bool live, const int (&m)[2], const float *x0, const float *w0, const float *x1,
                            const float *w1, float scale, const bool (&minus)[2], const QParams &p,
                            const uint64_t *grid, Iq1WS &ws, int (&gi)[2], bool (&og)[2]) {
@@ -172,18 +173,33 @@ struct KIQ1S : Iq8Tab<2048> {
             // a 33-entry array would not) and entry N, the totals, apart
             float sumx[N], sumw[N], totx, totw;
             sumx[0] = sumw[0] = 0;
+            {
+                // the elements in rank order through LDS: each element's (w*x, w) goes to its rank's slot of this
+                // lane's column of the wave's search workspace (unused until the searches below), then the slots are
+                // read back in rank order; 16 ranks a pass, the other pass's elements written to a 17th slot
+                float2 *slots = (float2 *)&ws;
+                const int lane = lane_id();
 #pragma unroll
-            for (int j = 0; j < N; ++j) {
-                float tx = 0.f, tw = 0.f;
+                for (int h = 0; h < 2; ++h) {
 #pragma unroll
-                for (int i = 0; i < N; ++i)
-                    if (R.get(i) == (uint32_t)j) { tx = weight[i] * x[i]; tw = weight[i]; }
-                if (j + 1 < N) {
-                    sumx[j + 1] = sumx[j] + tx;
-                    sumw[j + 1] = sumw[j] + tw;
-                } else {
-                    totx = sumx[j] + tx;
-                    totw = sumw[j] + tw;
+                    for (int i = 0; i < N; ++i) {
+                        const int r = (int)R.get(i) - 16 * h;
+                        slots[((unsigned)r < 16u ? r : 16) * 64 + lane] = make_float2(weight[i] * x[i], weight[i]);
+                    }
+                    wave_sync();
+#pragma unroll
+                    for (int jj = 0; jj < 16; ++jj) {
+                        const int j = 16 * h + jj;
+                        const float2 v = slots[jj * 64 + lane];
+                        if (j + 1 < N) {
+                            sumx[j + 1] = sumx[j] + v.x;
+                            sumw[j + 1] = sumw[j] + v.y;
+                        } else {
+                            totx = sumx[j] + v.x;
+                            totw = sumw[j] + v.y;
+                        }
+                    }
+                    wave_sync();
                 }
             }
             scale = mx;
@@ -327,17 +343,29 @@ struct KIQ1M : Iq8Tab<2048> {
             float px0[N + 1], px1[N + 1], pw0[N + 1], pw1[N + 1];
             px0[0] = px1[0] = 0;
             pw0[0] = pw1[0] = 0;
+            {
+                // the elements in rank order through LDS (as IQ1_S's prefix sums), with a mask of the ranks whose
+                // element lies in the second half
+                float2 *slots = (float2 *)&ws;
+                const int lane = lane_id();
+                uint32_t hm = 0;
 #pragma unroll
-            for (int j = 0; j < N; ++j) {
-                float tx = 0.f, tw = 0.f;
-                int hsel = 0;
+                for (int i = 0; i < N; ++i) {
+                    const uint32_t r = R.get(i);
+                    slots[r * 64 + lane] = make_float2(weight[i] * x[i], weight[i]);
+                    if (i >= N / 2) hm |= 1u << r;
+                }
+                wave_sync();
 #pragma unroll
-                for (int i = 0; i < N; ++i)
-                    if (R.get(i) == (uint32_t)j) { tx = weight[i] * x[i]; tw = weight[i]; hsel = i < N / 2 ? 0 : 1; }
-                px0[j + 1] = hsel == 0 ? px0[j] + tx : px0[j];
-                px1[j + 1] = hsel == 1 ? px1[j] + tx : px1[j];
-                pw0[j + 1] = hsel == 0 ? pw0[j] + tw : pw0[j];
-                pw1[j + 1] = hsel == 1 ? pw1[j] + tw : pw1[j];
+                for (int j = 0; j < N; ++j) {
+                    const float2 v = slots[j * 64 + lane];
+                    const int hsel = (int)((hm >> j) & 1u);
+                    px0[j + 1] = hsel == 0 ? px0[j] + v.x : px0[j];
+                    px1[j + 1] = hsel == 1 ? px1[j] + v.x : px1[j];
+                    pw0[j + 1] = hsel == 0 ? pw0[j] + v.y : pw0[j];
+                    pw1[j + 1] = hsel == 1 ? pw1[j] + v.y : pw1[j];
+                }
+                wave_sync();
             }
             const float txs0 = px0[N], txs1 = px1[N], tws0 = pw0[N], tws1 = pw1[N];
             const float p2 = xp2, m2 = xm2;
