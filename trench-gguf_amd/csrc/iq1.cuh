@@ -6,7 +6,9 @@
 //    the position of element i in glibc's stable order; the prefix sums then run in that order, serially, as ggml's.
 //  - The (i1, i2) partition search runs every candidate in ggml's order on the lane, so its cross-multiplied
 //    acceptance chain is ggml's exactly. Its loop indices are wave-uniform, so the prefix arrays are indexed through
-//    uniform (M0-relative) register addressing.
+//    uniform (M0-relative) register addressing. IQ1_M first ranks the candidates by an approximate score, without
+//    branches; where the best stands clear of the rest by more than the rounding can move them, it is the chain's
+//    last accept (iq1_rank_ok), and only the other lanes run the chain.
 //  - IQ1_M's final least-squares d over all 256 weights is a lane-to-lane chain in ggml's index order.
 //  - The neighbour searches of the final points run wave-wide (coop.cuh), so every lane takes part in them.
 // Tables: the 2048-point IQ1 grid and its base-3 key map in LDS (the IQ1 levels are always 0..2), lists in HBM.
@@ -105,6 +107,25 @@ template <int N> DEV bool iq1_weights_plain(const float (&w)[N], bool &any) {
         any = any || w[i] > 0.f;
     }
     return ok;
+}
+
+// Whether IQ1_M's ranking pass settles a lane's partition scan. ggml's chain accepts a candidate c when
+// fl(sumqx_c^2) > fl(best * sumq2_c), best = fl(fl(sumqx_r / sumq2_r) * sumqx_r) of the last accepted r (at first
+// -FLT_MAX); with T(c) = sumqx_c^2 / sumq2_c over the candidates' own float sums, that test reads
+// T(c) (1 + e) > T(r) (1 + e1) (1 + e2) (1 + e3), |e*| <= u = 2^-24, while the products stay in the normal range.
+// The ranking pass's score A(c) = fl(fl(sumqx_c^2) rcp(sumq2_c)) is T(c) within 4u (rcp: 1 ulp). If the largest
+// score S1 exceeds the second S2 by the factor fl(1 + 2^-20) (at least 1 + 15u), its candidate c* has
+// T(c*) > T(c) (1 + 6u) for every other c: the chain accepts c* when it reaches it (whatever record precedes it) and
+// nothing after it, so c* is the last accept, and its scale is fl(sumqx* / sumq2*) as the chain computes it. The
+// range conditions: weights 0 or in [2^-100, 2^100] with a total in [2^-40, 2^40] (every sumq2 is then >= 2^-47: each
+// weight's q^2 is >= 1/64, the sums' rounding far below that, so every candidate has sumq2 > 0 as the chain requires),
+// max|x| * total <= 2^50 (sumqx^2 <= 2^101 and best * sumq2 <= 81 sumqx*^2: no overflow), and S1 in [2^-60, 2^100]
+// (the comparisons that accept c* or reject the candidates after it stay normal; a losing candidate's square may
+// underflow, which only lowers it). A lane outside them, or whose top two are closer (near ties, exact ties from zero
+// weights), replays the chain.
+DEV bool iq1_rank_ok(bool wplain, float totw, float mx, float S1, float S2) {
+    return wplain && totw >= 0x1p-40f && totw <= 0x1p40f && mx * totw <= 0x1p50f && S1 >= 0x1p-60f &&
+           S1 <= 0x1p100f && S1 > S2 * (1.f + 0x1p-20f);
 }
 
 // position of element i in the stable ascending order of x
@@ -312,6 +333,41 @@ struct KIQ1S : Iq8Tab<2048> {
 };
 
 // ------------------------------------------------------------------ IQ1_M (gpuq/gpuq.hip:516-688)
+// The sums of one (i1, i2) candidate of IQ1_M's partition scan for its four shift combinations k (bit 1: the first
+// half's shift is -1, bit 0: the second half's), from the halves' prefix sums at i1 (a*) and i2 (b*) and their totals
+// (t*), in the operation order of gpuq/gpuq.hip:579-604
+DEV void iq1m_sums(float a0x, float a1x, float a0w, float a1w, float b0x, float b1x, float b0w, float b1w, float txs0,
+                   float txs1, float tws0, float tws1, float (&sumqx)[4], float (&sumq2)[4]) {
+    const float xp0 = -1 + IQ1_DELTA, xp1 = IQ1_DELTA, xp2 = 1 + IQ1_DELTA;
+    const float xm0 = -1 - IQ1_DELTA, xm1 = -IQ1_DELTA, xm2 = 1 - IQ1_DELTA;
+    const float p2 = xp2, m2 = xm2;
+    const float cp1 = xp0 * xp0 - xp1 * xp1, cp2 = xp1 * xp1 - xp2 * xp2;
+    const float cm1 = xm0 * xm0 - xm1 * xm1, cm2 = xm1 * xm1 - xm2 * xm2;
+    float qx_p[2], qx_m[2], q2_p[2], q2_m[2];
+    {
+        const float sx = a0x + b0x;
+        qx_p[0] = txs0 * p2 - sx;
+        qx_m[0] = txs0 * m2 - sx;
+        q2_p[0] = tws0 * p2 * p2 + a0w * cp1 + b0w * cp2;
+        q2_m[0] = tws0 * m2 * m2 + a0w * cm1 + b0w * cm2;
+    }
+    {
+        const float sx = a1x + b1x;
+        qx_p[1] = txs1 * p2 - sx;
+        qx_m[1] = txs1 * m2 - sx;
+        q2_p[1] = tws1 * p2 * p2 + a1w * cp1 + b1w * cp2;
+        q2_m[1] = tws1 * m2 * m2 + a1w * cm1 + b1w * cm2;
+    }
+    sumqx[0] = qx_p[0] + qx_p[1];
+    sumqx[1] = qx_p[0] + qx_m[1];
+    sumqx[2] = qx_m[0] + qx_p[1];
+    sumqx[3] = qx_m[0] + qx_m[1];
+    sumq2[0] = q2_p[0] + q2_p[1];
+    sumq2[1] = q2_p[0] + q2_m[1];
+    sumq2[2] = q2_m[0] + q2_p[1];
+    sumq2[3] = q2_m[0] + q2_m[1];
+}
+
 // block: qs[32] qh[16] scales[8] (56 bytes); lane g = 16-weight block g
 struct KIQ1M : Iq8Tab<2048> {
     static constexpr int BS = QK, G = 16, N = 16, BB = 56, WS = coop_wsm_bytes<2, 16, true>(), WGW = 8;
@@ -320,8 +376,6 @@ struct KIQ1M : Iq8Tab<2048> {
                           const QParams &p) {
         const uint64_t *grid = Iq8Tab<2048>::grid(lds);
         const int32_t *map3 = Iq8Tab<2048>::map3(lds);
-        const float xp0 = -1 + IQ1_DELTA, xp1 = IQ1_DELTA, xp2 = 1 + IQ1_DELTA;
-        const float xm0 = -1 - IQ1_DELTA, xm1 = -IQ1_DELTA, xm2 = 1 - IQ1_DELTA;
         float qv[N], sq[N], weight[N];
         load_qw<N>(qwp, qv);
 #pragma unroll
@@ -368,50 +422,83 @@ struct KIQ1M : Iq8Tab<2048> {
                 wave_sync();
             }
             const float txs0 = px0[N], txs1 = px1[N], tws0 = pw0[N], tws1 = pw1[N];
-            const float p2 = xp2, m2 = xm2;
-            const float cp1 = xp0 * xp0 - xp1 * xp1, cp2 = xp1 * xp1 - xp2 * xp2;
-            const float cm1 = xm0 * xm0 - xm1 * xm1, cm2 = xm1 * xm1 - xm2 * xm2;
-            float best_score = -FLT_MAX;
             scale = mx;
             int besti1 = -1, besti2 = -1, bk = -1;
-            // i1 rolled (its prefix values read once an iteration), i2 unrolled with a uniform skip below i1: every
-            // prefix read in the inner body is a fixed register
-            for (int i1 = 0; i1 <= N; ++i1) {
-                const float a0x = px0[i1], a1x = px1[i1], a0w = pw0[i1], a1w = pw1[i1];
+            // The ranking pass (see iq1_rank_ok): every candidate's score sumqx^2 / sumq2 approximated without a
+            // branch, the two largest kept with the largest's candidate; a lane whose largest stands clear of the
+            // second takes it as the chain's last accept, the others replay the chain below.
+            bool ok;
+            {
+                bool wany;
+                const bool wplain = iq1_weights_plain<N>(weight, wany);
+                const float totw = tws0 + tws1;
+                // the largest's candidate: its i1 (set when an i1 iteration raised the largest) and its 4 i2 + k
+                // (an inline constant in the select once offset by -16)
+                float S1 = -1.f, S2 = -1.f;
+                int si1 = 0, sik = 0;
+                for (int i1 = 0; i1 <= N; ++i1) {
+                    const float a0x = px0[i1], a1x = px1[i1], a0w = pw0[i1], a1w = pw1[i1];
+                    const float S1in = S1;
 #pragma unroll
-                for (int i2 = 0; i2 <= N; ++i2) {
-                    if (i2 < i1) continue;
-                    float qx_p[2], qx_m[2], q2_p[2], q2_m[2];
-                    {
-                        const float sx = a0x + px0[i2];
-                        qx_p[0] = txs0 * p2 - sx;
-                        qx_m[0] = txs0 * m2 - sx;
-                        q2_p[0] = tws0 * p2 * p2 + a0w * cp1 + pw0[i2] * cp2;
-                        q2_m[0] = tws0 * m2 * m2 + a0w * cm1 + pw0[i2] * cm2;
+                    for (int i2 = 0; i2 <= N; ++i2) {
+                        if (i2 < i1) continue;
+                        float sumqx[4], sumq2[4];
+                        iq1m_sums(a0x, a1x, a0w, a1w, px0[i2], px1[i2], pw0[i2], pw1[i2], txs0, txs1, tws0, tws1,
+                                  sumqx, sumq2);
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            const float A = sumqx[k] * sumqx[k] * __builtin_amdgcn_rcpf(sumq2[k]);
+                            sik = A > S1 ? 4 * i2 + k - 16 : sik;
+                            S2 = __builtin_amdgcn_fmed3f(S1, S2, A);      // (S1 >= S2: the second of the three)
+                            S1 = fmaxf(S1, A);                            // (no NaN where the result is used)
+                        }
                     }
-                    {
-                        const float sx = a1x + px1[i2];
-                        qx_p[1] = txs1 * p2 - sx;
-                        qx_m[1] = txs1 * m2 - sx;
-                        q2_p[1] = tws1 * p2 * p2 + a1w * cp1 + pw1[i2] * cp2;
-                        q2_m[1] = tws1 * m2 * m2 + a1w * cm1 + pw1[i2] * cm2;
+                    si1 = S1 > S1in ? i1 : si1;
+                }
+                ok = iq1_rank_ok(wplain, totw, mx, S1, S2);
+                if (ok) {
+                    besti1 = si1;
+                    besti2 = (sik + 16) >> 2;
+                    bk = (sik + 16) & 3;
+                    // the winner's sums again (the same operations on the same prefix values), its scale as the
+                    // chain computes it
+                    float a[4] = {0.f, 0.f, 0.f, 0.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int j = 0; j <= N; ++j) {
+                        if (j == besti1) { a[0] = px0[j]; a[1] = px1[j]; a[2] = pw0[j]; a[3] = pw1[j]; }
+                        if (j == besti2) { b[0] = px0[j]; b[1] = px1[j]; b[2] = pw0[j]; b[3] = pw1[j]; }
                     }
                     float sumqx[4], sumq2[4];
-                    sumqx[0] = qx_p[0] + qx_p[1];
-                    sumqx[1] = qx_p[0] + qx_m[1];
-                    sumqx[2] = qx_m[0] + qx_p[1];
-                    sumqx[3] = qx_m[0] + qx_m[1];
-                    sumq2[0] = q2_p[0] + q2_p[1];
-                    sumq2[1] = q2_p[0] + q2_m[1];
-                    sumq2[2] = q2_m[0] + q2_p[1];
-                    sumq2[3] = q2_m[0] + q2_m[1];
+                    iq1m_sums(a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3], txs0, txs1, tws0, tws1, sumqx, sumq2);
+                    float bx = sumqx[0], b2 = sumq2[0];
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        // (both tests evaluated: one branch instead of two nested ones; the second has no effects)
-                        if ((sumq2[k] > 0) & (sumqx[k] * sumqx[k] > best_score * sumq2[k])) {
-                            scale = sumqx[k] / sumq2[k];
-                            best_score = scale * sumqx[k];
-                            besti1 = i1; besti2 = i2; bk = k;
+                    for (int k = 1; k < 4; ++k) {
+                        if (k == bk) { bx = sumqx[k]; b2 = sumq2[k]; }
+                    }
+                    scale = bx / b2;
+                }
+            }
+            // ggml's acceptance chain for the lanes the ranking could not settle: i1 rolled (its prefix values read
+            // once an iteration), i2 unrolled with a uniform skip below i1: every prefix read in the inner body is a
+            // fixed register
+            if (__ballot(!ok)) {
+                float best_score = ok ? __builtin_inff() : -FLT_MAX;     // (a settled lane accepts nothing here)
+                for (int i1 = 0; i1 <= N; ++i1) {
+                    const float a0x = px0[i1], a1x = px1[i1], a0w = pw0[i1], a1w = pw1[i1];
+#pragma unroll
+                    for (int i2 = 0; i2 <= N; ++i2) {
+                        if (i2 < i1) continue;
+                        float sumqx[4], sumq2[4];
+                        iq1m_sums(a0x, a1x, a0w, a1w, px0[i2], px1[i2], pw0[i2], pw1[i2], txs0, txs1, tws0, tws1,
+                                  sumqx, sumq2);
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            // (both tests evaluated: one branch instead of two nested ones; the second has no effects)
+                            if ((sumq2[k] > 0) & (sumqx[k] * sumqx[k] > best_score * sumq2[k])) {
+                                scale = sumqx[k] / sumq2[k];
+                                best_score = scale * sumqx[k];
+                                besti1 = i1; besti2 = i2; bk = k;
+                            }
                         }
                     }
                 }
