@@ -26,6 +26,13 @@ DEV int imax(int a, int b) { return a > b ? a : b; }
 DEV int imin(int a, int b) { return a < b ? a : b; }
 // make v opaque to the optimizer at this point (no instruction): expressions of v are not hoisted across it
 DEV void opaque(float &v) { asm volatile("" : "+v"(v)); }
+// hide a float holding a small non-negative integer from the optimizer (no instruction), so that q * q stays one float
+// multiply (exact below 2^12): left to itself the compiler squares the integer instead, with v_mul_u32_u24 and
+// v_cvt_f32_u32, both four-clock instructions, where v_mul_f32 issues at twice their rate
+DEV float small_int_f(float q) {
+    asm("" : "+v"(q));
+    return q;
+}
 
 // RNE fp32 -> fp16 through the fp32 adder; NaN -> 0x7E00
 DEV uint16_t f2h(float f) {

@@ -230,7 +230,7 @@ DEV void coop_filter(const int (&cnt)[W], const int (&off)[W], const int (&ntr)[
             float A = 0.f, B = 0.f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const float q = (float)(((i < 4 ? lo : hi) >> (8 * (i % 4))) & 0xffu);
+                const float q = small_int_f((float)(((i < 4 ? lo : hi) >> (8 * (i % 4))) & 0xffu));
                 A = fmaf(w[i], q * q, A);
                 B = fmaf(wx[i], q, B);
             }
