@@ -374,24 +374,31 @@ DEV float affine_levels(int nmax, const float (&x)[N], const float (&w)[N], Lv<N
         diff = use_mad ? fabsf(diff) : diff * diff;
         best += w[i] * diff;
     }
+    // The trials keep their levels as floats; the accepted trial's (iscale, min) are kept and its levels formed again
+    // after the loop (the same operations on the same values), instead of packing every trial's levels. With the
+    // imatrix the level is formed in float: for v > 0, nint(min(v, nmax)) is the integer that min(v, nmax) + 1.5*2^23
+    // rounds to (|min(v, nmax)| < 2^22), so (min(v, nmax) + 1.5*2^23) - 1.5*2^23 is its exact value; v <= 0 or NaN
+    // gives 0 through the select, and min(NaN, nmax) = nmax as ggml's `v < nmax ? v : nmax` (two-clock adds in place of
+    // the integer extraction and conversion, four-clock instructions).
+    constexpr float RND = 12582912.f;
+    float acc_is = 0.f, acc_mn = 0.f;
+    bool acc = false;
     for (int is = 0; is <= nstep; ++is) {
         iscale = (rmin + rdelta * is + nmax) / (mx - mn);
         float sum_l = 0, sum_l2 = 0, sum_xl = 0;
-        Lv<N> La;
+        float lf[N];
 #pragma unroll
         for (int i = 0; i < N; ++i) {
-            int l;
             if (WI) {
                 const float v = iscale * (x[i] - mn);
-                l = v > 0 ? nint(v < nmax ? v : (float)nmax) : 0;
+                const float r = (fminf(v, (float)nmax) + RND) - RND;
+                lf[i] = v > 0 ? r : 0.f;
             } else {
-                l = imax(0, imin(nmax, nint(iscale * (x[i] - mn))));
+                lf[i] = (float)imax(0, imin(nmax, nint(iscale * (x[i] - mn))));
             }
-            if (i % 4 == 0) La.w[i / 4] = 0u;
-            La.w[i / 4] |= (uint32_t)l << (8 * (i % 4));
-            sum_l += w[i] * l;
-            sum_l2 += w[i] * l * l;
-            sum_xl += w[i] * l * x[i];
+            sum_l += w[i] * lf[i];
+            sum_l2 += w[i] * lf[i] * lf[i];
+            sum_xl += w[i] * lf[i] * x[i];
         }
         const float D = sum_w * sum_l2 - sum_l * sum_l;
         if (!(D > 0)) continue;
@@ -404,15 +411,30 @@ DEV float affine_levels(int nmax, const float (&x)[N], const float (&w)[N], Lv<N
         float err = 0;
 #pragma unroll
         for (int i = 0; i < N; ++i) {
-            float diff = this_scale * (float)La.get(i) + this_min - x[i];
+            float diff = this_scale * lf[i] + this_min - x[i];
             diff = use_mad ? fabsf(diff) : diff * diff;
             err += w[i] * diff;
         }
         if (err < best) {
-            L = La;
+            acc = true;
+            acc_is = iscale;
+            acc_mn = mn;
             best = err;
             scale = this_scale;
             mn = this_min;
+        }
+    }
+    if (acc) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            int l;
+            if (WI) {
+                const float v = acc_is * (x[i] - acc_mn);
+                l = v > 0 ? nint(v < nmax ? v : (float)nmax) : 0;
+            } else {
+                l = imax(0, imin(nmax, nint(acc_is * (x[i] - acc_mn))));
+            }
+            L.put(i, (uint32_t)l);
         }
     }
     the_min = -mn;
