@@ -133,3 +133,55 @@ def test_negative_importance_iq1(oracle_lib, typ):
     out = d_out.cpu().numpy()
     assert np.array_equal(out, want), "%d bytes differ" % int((out != want).sum())
     assert gq.gpuq_take_error() == 0
+
+
+KQ = [10, 11, 12, 13, 14]
+KQ_LANES = {10: 16, 11: 16, 12: 8, 13: 8, 14: 16}      # lanes a super-block: a wave holds 64 / lanes super-blocks
+
+
+def mixed_wave_case(typ, seed=3):
+    """a NaN and an infinite value in two super-blocks of their waves; every other super-block finite"""
+    rng = np.random.default_rng(seed + typ)
+    x = (rng.standard_normal((8, 2048)) * 0.02).astype(np.float32)
+    x[1, 37] = np.nan
+    x[5, 1500] = np.inf
+    im = rng.lognormal(0.0, 1.5, 2048).astype(np.float32)
+    return x, im
+
+
+def test_mixed_waves_hold_finite_super_blocks():
+    for typ in KQ:
+        x, _ = mixed_wave_case(typ)
+        sb = x.reshape(-1, 256)
+        bad = ~np.isfinite(sb).all(1)
+        waves = bad.reshape(-1, 64 // KQ_LANES[typ])
+        mixed = waves.any(1) & ~waves.all(1)
+        assert mixed.sum() == 2 and not waves[~mixed].any(), typ
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("with_im", [False, True], ids=["plain", "imatrix"])
+@pytest.mark.parametrize("typ", KQ, ids=[NAMES[t] for t in KQ])
+def test_finite_super_blocks_beside_non_finite(oracle_lib, typ, with_im):
+    """A wave holding a NaN or an infinite value rounds its symmetric trials with the integer loop (the others in
+    float, csrc/kquants.cuh sym_levels); the super-blocks without such values are the oracle's bytes either way."""
+    import torch
+    torch.cuda.init()
+    import gpuq
+    gq = gpuq.load_gpuq(0)
+    x, im = mixed_wave_case(typ)
+    im = im if with_im else None
+    want = oracle_lib.quantize(typ, x, im).reshape(-1)
+    bb = gq.gpuq_block_bytes(typ)
+    d_x = torch.from_numpy(x).cuda()
+    d_im = None if im is None else torch.from_numpy(im).cuda()
+    d_out = torch.zeros(want.size, dtype=torch.uint8, device="cuda")
+    print("case mixed waves %s %s" % (NAMES[typ], "imatrix" if with_im else "plain"), flush=True)
+    n = gq.gpuq_requantize_dev(0, d_x.data_ptr(), typ, d_out.data_ptr(), 1, x.shape[0], x.shape[1],
+                               None if d_im is None else d_im.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert n == want.size
+    gq.gpuq_take_error()
+    fin = np.isfinite(x.reshape(-1, 256)).all(1)
+    out = d_out.cpu().numpy().reshape(-1, bb)
+    assert np.array_equal(out[fin], want.reshape(-1, bb)[fin])

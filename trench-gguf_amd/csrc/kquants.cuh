@@ -214,6 +214,42 @@ template <int N> DEV float sym_levels(int nmax, const float (&x)[N], Lv<N> &L, c
     }
     float scale = suml2 ? sumlx / suml2 : 0.0f;
     float best = scale * sumlx;
+    // A wave whose values are all finite forms the trials' levels in float: |iscale * x| <= nmax + 0.9 (mx has the
+    // largest magnitude), and below 2^22 nint(v) is (v + 1.5*2^23) - 1.5*2^23, so clamping v to the integer bounds
+    // first gives the clamped level exactly (two-clock adds in place of the integer extraction and conversion); the
+    // accepted trial's levels are formed again after the loop. (A NaN or infinite value, which ggml's integer rounding
+    // maps to level 0 or -nmax, keeps the integer loop below.)
+    bool fin = true;
+#pragma unroll
+    for (int i = 0; i < N; ++i) fin = fin && __builtin_isfinite(x[i]);
+    if (!__ballot(!fin)) {
+        constexpr float RND = 12582912.f;
+        const float lo = (float)-nmax, hi = (float)(nmax - 1);
+        float acc_is = 0.f;
+        bool acc = false;
+        for (int is = -9; is <= 9; ++is) {
+            if (is == 0) continue;
+            iscale = -(nmax + 0.1f * is) / mx;
+            sumlx = suml2 = 0;
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+                const float lf = (fminf(fmaxf(iscale * x[i], lo), hi) + RND) - RND;
+                sumlx += wv[i] * x[i] * lf;
+                suml2 += wv[i] * lf * lf;
+            }
+            if (suml2 > 0 && sumlx * sumlx > best * suml2) {
+                acc = true;
+                acc_is = iscale;
+                scale = sumlx / suml2;
+                best = scale * sumlx;
+            }
+        }
+        if (acc) {
+#pragma unroll
+            for (int i = 0; i < N; ++i) L.put(i, (uint32_t)(imax(-nmax, imin(nmax - 1, nint(acc_is * x[i]))) + nmax));
+        }
+        return scale;
+    }
     for (int is = -9; is <= 9; ++is) {
         if (is == 0) continue;
         iscale = -(nmax + 0.1f * is) / mx;
