@@ -412,10 +412,10 @@ DEV float affine_levels(int nmax, const float (&x)[N], const float (&w)[N], Lv<N
     }
     // The trials keep their levels as floats; the accepted trial's (iscale, min) are kept and its levels formed again
     // after the loop (the same operations on the same values), instead of packing every trial's levels. With the
-    // imatrix the level is formed in float: for v > 0, nint(min(v, nmax)) is the integer that min(v, nmax) + 1.5*2^23
-    // rounds to (|min(v, nmax)| < 2^22), so (min(v, nmax) + 1.5*2^23) - 1.5*2^23 is its exact value; v <= 0 or NaN
-    // gives 0 through the select, and min(NaN, nmax) = nmax as ggml's `v < nmax ? v : nmax` (two-clock adds in place of
-    // the integer extraction and conversion, four-clock instructions).
+    // imatrix the level is formed in float: ggml's `v > 0 ? nint(v < nmax ? v : nmax) : 0` is nint(c) for
+    // c = min(max(v, 0), nmax) (IEEE max and min: v <= 0, -inf and NaN give 0, +inf gives nmax), and with 0 <= c <= nmax
+    // nint(c) is the integer that c + 1.5*2^23 rounds to, so (c + 1.5*2^23) - 1.5*2^23 is its exact value: one clamp
+    // and two two-clock adds in place of the compare, select, integer extraction and conversion.
     constexpr float RND = 12582912.f;
     float acc_is = 0.f, acc_mn = 0.f;
     bool acc = false;
@@ -426,9 +426,7 @@ DEV float affine_levels(int nmax, const float (&x)[N], const float (&w)[N], Lv<N
 #pragma unroll
         for (int i = 0; i < N; ++i) {
             if (WI) {
-                const float v = iscale * (x[i] - mn);
-                const float r = (fminf(v, (float)nmax) + RND) - RND;
-                lf[i] = v > 0 ? r : 0.f;
+                lf[i] = (fminf(fmaxf(iscale * (x[i] - mn), 0.f), (float)nmax) + RND) - RND;
             } else {
                 lf[i] = (float)imax(0, imin(nmax, nint(iscale * (x[i] - mn))));
             }
