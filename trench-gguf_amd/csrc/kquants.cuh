@@ -215,10 +215,10 @@ template <int N> DEV float sym_levels(int nmax, const float (&x)[N], Lv<N> &L, c
     float scale = suml2 ? sumlx / suml2 : 0.0f;
     float best = scale * sumlx;
     // A wave whose values are all finite forms the trials' levels in float: |iscale * x| <= nmax + 0.9 (mx has the
-    // largest magnitude), and below 2^22 nint(v) is (v + 1.5*2^23) - 1.5*2^23, so clamping v to the integer bounds
-    // first gives the clamped level exactly (two-clock adds in place of the integer extraction and conversion); the
-    // accepted trial's levels are formed again after the loop. (A NaN or infinite value, which ggml's integer rounding
-    // maps to level 0 or -nmax, keeps the integer loop below.)
+    // largest magnitude), and for |v| <= 2^21 nint(v) is (v + 1.5*2^23) - 1.5*2^23, so clamping v to the integer
+    // bounds first gives the clamped level exactly (two-clock adds in place of the integer extraction and
+    // conversion); the accepted trial's levels are formed again after the loop. (A NaN or infinite value, whose level
+    // ggml's integer rounding takes from its bits, keeps the integer loop below.)
     bool fin = true;
 #pragma unroll
     for (int i = 0; i < N; ++i) fin = fin && __builtin_isfinite(x[i]);
