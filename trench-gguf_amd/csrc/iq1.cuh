@@ -432,10 +432,11 @@ struct KIQ1M : Iq8Tab<2048> {
                 bool wany;
                 const bool wplain = iq1_weights_plain<N>(weight, wany);
                 const float totw = tws0 + tws1;
-                // the largest's candidate: its i1 (set when an i1 iteration raised the largest) and its 4 i2 + k
-                // (an inline constant in the select once offset by -16)
+                // the largest's candidate: its i1 (set when an i1 iteration raised the largest) and its i2 (set when
+                // the pair's four candidates raised it); its k is found after the pass, as the first of the pair's
+                // four scores, formed again, that equals the largest (the first to reach it is the last raise)
                 float S1 = -1.f, S2 = -1.f;
-                int si1 = 0, sik = 0;
+                int si1 = 0, si2 = 0;
                 for (int i1 = 0; i1 <= N; ++i1) {
                     const float a0x = px0[i1], a1x = px1[i1], a0w = pw0[i1], a1w = pw1[i1];
                     const float S1in = S1;
@@ -445,23 +446,23 @@ struct KIQ1M : Iq8Tab<2048> {
                         float sumqx[4], sumq2[4];
                         iq1m_sums(a0x, a1x, a0w, a1w, px0[i2], px1[i2], pw0[i2], pw1[i2], txs0, txs1, tws0, tws1,
                                   sumqx, sumq2);
+                        const float S1p = S1;
 #pragma unroll
                         for (int k = 0; k < 4; ++k) {
                             const float A = sumqx[k] * sumqx[k] * __builtin_amdgcn_rcpf(sumq2[k]);
-                            sik = A > S1 ? 4 * i2 + k - 16 : sik;
                             S2 = __builtin_amdgcn_fmed3f(S1, S2, A);      // (S1 >= S2: the second of the three)
                             S1 = fmaxf(S1, A);                            // (no NaN where the result is used)
                         }
+                        si2 = S1 > S1p ? i2 : si2;
                     }
                     si1 = S1 > S1in ? i1 : si1;
                 }
                 ok = iq1_rank_ok(wplain, totw, mx, S1, S2);
                 if (ok) {
                     besti1 = si1;
-                    besti2 = (sik + 16) >> 2;
-                    bk = (sik + 16) & 3;
-                    // the winner's sums again (the same operations on the same prefix values), its scale as the
-                    // chain computes it
+                    besti2 = si2;
+                    // the winner's sums again (the same operations on the same prefix values), its shift pair k and
+                    // its scale as the chain computes it
                     float a[4] = {0.f, 0.f, 0.f, 0.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int j = 0; j <= N; ++j) {
@@ -470,6 +471,10 @@ struct KIQ1M : Iq8Tab<2048> {
                     }
                     float sumqx[4], sumq2[4];
                     iq1m_sums(a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3], txs0, txs1, tws0, tws1, sumqx, sumq2);
+                    bk = 3;
+#pragma unroll
+                    for (int k = 2; k >= 0; --k)
+                        if (sumqx[k] * sumqx[k] * __builtin_amdgcn_rcpf(sumq2[k]) == S1) bk = k;
                     float bx = sumqx[0], b2 = sumq2[0];
 #pragma unroll
                     for (int k = 1; k < 4; ++k) {
