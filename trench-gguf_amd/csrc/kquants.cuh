@@ -635,7 +635,6 @@ struct KQ3K {
 // block: d dmin scales[12] then Q4_K qs[128] (144 bytes) / Q5_K qh[32] qs[128] (176 bytes); lane g = 32 weights
 template <int NMAX> struct KQ45K {
     static constexpr int BS = QK, G = 8, N = 32, BB = NMAX == 15 ? 144 : 176, TAB = 0;
-    static constexpr int WPE = 3;    // three waves a SIMD (168 VGPRs, 180 bytes a lane of spill): 4% faster than two
     static DEV void stage(const QParams &, uint8_t *) {}
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *,
                           const QParams &) {
