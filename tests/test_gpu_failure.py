@@ -150,11 +150,11 @@ def mixed_wave_case(typ, seed=3):
 
 
 def test_mixed_waves_hold_finite_super_blocks():
-    for typ in KQ:
+    for typ in KQ + [16]:
         x, _ = mixed_wave_case(typ)
         sb = x.reshape(-1, 256)
         bad = ~np.isfinite(sb).all(1)
-        waves = bad.reshape(-1, 64 // KQ_LANES[typ])
+        waves = bad.reshape(-1, 64 // (8 if typ == 16 else KQ_LANES[typ]))
         mixed = waves.any(1) & ~waves.all(1)
         assert mixed.sum() == 2 and not waves[~mixed].any(), typ
 
@@ -183,5 +183,34 @@ def test_finite_super_blocks_beside_non_finite(oracle_lib, typ, with_im):
     assert n == want.size
     gq.gpuq_take_error()
     fin = np.isfinite(x.reshape(-1, 256)).all(1)
+    out = d_out.cpu().numpy().reshape(-1, bb)
+    assert np.array_equal(out[fin], want.reshape(-1, bb)[fin])
+
+
+@pytest.mark.gpu
+def test_iq2_xxs_finite_super_blocks_beside_non_finite(oracle_lib):
+    """IQ2_XXS super-blocks without a NaN or infinite value, in waves (8 super-blocks) that hold one, are the oracle's
+    bytes, taken from the oracle on the same rows with the non-finite values set to 0 (a super-block's bytes depend
+    only on its own values and importances): the wave-wide searches a non-finite group takes part in leave its
+    neighbours' results alone."""
+    import torch
+    torch.cuda.init()
+    import gpuq
+    gq = gpuq.load_gpuq(0)
+    typ = 16
+    x, im = mixed_wave_case(typ)
+    want = oracle_lib.quantize(typ, np.where(np.isfinite(x), x, 0).astype(np.float32), im).reshape(-1)
+    bb = gq.gpuq_block_bytes(typ)
+    d_x = torch.from_numpy(x).cuda()
+    d_im = torch.from_numpy(im).cuda()
+    d_out = torch.zeros(want.size, dtype=torch.uint8, device="cuda")
+    print("case mixed waves iq2_xxs imatrix", flush=True)
+    n = gq.gpuq_requantize_dev(0, d_x.data_ptr(), typ, d_out.data_ptr(), 1, x.shape[0], x.shape[1], d_im.data_ptr(),
+                               torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert n == want.size
+    gq.gpuq_take_error()
+    fin = np.isfinite(x.reshape(-1, 256)).all(1)
+    assert fin.sum() == fin.size - 2
     out = d_out.cpu().numpy().reshape(-1, bb)
     assert np.array_equal(out[fin], want.reshape(-1, bb)[fin])
