@@ -12,7 +12,8 @@ HEADER = os.path.join(ROOT, "include", "gpuq.h")
 
 
 def header_functions():
-    src = open(HEADER).read()
+    with open(HEADER) as f:
+        src = f.read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
     return re.findall(r"\b(?:int|size_t)\s+(gpuq_\w+)\s*\(", src)
 
