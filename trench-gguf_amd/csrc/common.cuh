@@ -22,6 +22,8 @@ DEV uint32_t fbits(float f) { return __float_as_uint(f); }
 DEV float ffrom(uint32_t u) { return __uint_as_float(u); }
 DEV float fmax_sel(float a, float b) { return a > b ? a : b; }   // ggml's MAX macro: a > b ? a : b
 DEV float fmin_sel(float a, float b) { return a < b ? a : b; }
+// a compile-time int as a type (a generic lambda's size parameter)
+template <int V> struct IntC { static constexpr int value = V; };
 DEV int imax(int a, int b) { return a > b ? a : b; }
 DEV int imin(int a, int b) { return a < b ? a : b; }
 // make v opaque to the optimizer at this point (no instruction): expressions of v are not hoisted across it

@@ -248,7 +248,7 @@ DEV void window_group(const float (&xk)[8], const float (&waux)[8], const float 
 struct KIQ2XXS : Iq8Tab<256> {
     static constexpr int BS = QK, G = 8, N = 32, BB = 66, NTRIAL = 13;
     static constexpr bool QUEUE = true;         // (tiles of varying cost: the tile queue)
-    static constexpr int TW = 7;        // trials a window: windows 0..6 and 7..12
+    static constexpr int TW = 7;        // trials a window: windows 0..6 and 7..12 (the second of 6)
     // per-wave LDS: the search workspace, shared by the filtered, the 4-list, the 2-list and the 1-list searches and
     // their staged values; eight waves a workgroup share one copy of the tables (the workspace would not let two
     // four-wave workgroups share a CU's LDS)
@@ -299,18 +299,21 @@ struct KIQ2XXS : Iq8Tab<256> {
         float best = 0;
         int tacc = -1;          // the last accepted trial (-1: none), its inverse scale and scale
         float acc_id = 0.f, acc_sc = 0.f;
-#pragma unroll 1
-        for (int w0 = 0; w0 < NTRIAL; w0 += TW) {
-            float idv[TW], tsv[TW], sqx[TW], sq2[TW];
+        // (a window of W trials from trial w0: the first of TW, the second of the NTRIAL - TW left, so that no walk
+        // evaluates a trial past the last)
+        auto window = [&](auto wc, int w0) {
+            constexpr int W = decltype(wc)::value;
+            FiltWS<W> &fw = *(FiltWS<W> *)&fws;
+            float idv[W], tsv[W], sqx[W], sq2[W];
 #pragma unroll
-            for (int m = 0; m < TW; ++m) {
+            for (int m = 0; m < W; ++m) {
                 idv[m] = (5 + (w0 + m - 6) * 0.1f) / eff_max;
                 tsv[m] = 1 / idv[m];
                 sqx[m] = sq2[m] = 0.f;
             }
             unsigned valid = 0;
 #pragma unroll
-            for (int m = 0; m < TW; ++m)
+            for (int m = 0; m < W; ++m)
                 if (live && w0 + m < NTRIAL) valid |= 1u << m;
 #pragma unroll 1
             for (int k = 0; k < 4; ++k) {       // (not unrolled: one copy of the search code, groups kept apart)
@@ -320,17 +323,17 @@ struct KIQ2XXS : Iq8Tab<256> {
                     xk[i] = xval[i];
                     waux[i] = sqrtf(weight[i]);
                 }
-                int gk[TW];                     // the trials' grid indices of group k
+                int gk[W];                     // the trials' grid indices of group k
                 unsigned og;
-                window_group<TW, 8, 256>(xk, waux, idv, tsv, valid, map3, p, grid, fws, ws, wsm, gk, og);
+                window_group<W, 8, 256>(xk, waux, idv, tsv, valid, map3, p, grid, fw, ws, wsm, gk, og);
 #pragma unroll
-                for (int m = 0; m < TW; ++m) sums_q8(weight, xval, grid[gk[m]], sqx[m], sq2[m]);
+                for (int m = 0; m < W; ++m) sums_q8(weight, xval, grid[gk[m]], sqx[m], sq2[m]);
                 rot8(xval);
                 rot8(weight);
             }
             // the acceptance chain over the window's trials, in ggml's order
 #pragma unroll
-            for (int m = 0; m < TW; ++m) {
+            for (int m = 0; m < W; ++m) {
                 if (w0 + m < NTRIAL && live && sq2[m] > 0 && sqx[m] * sqx[m] > best * sq2[m]) {
                     scale = sqx[m] / sq2[m];
                     best = scale * sqx[m];
@@ -339,7 +342,9 @@ struct KIQ2XXS : Iq8Tab<256> {
                     acc_sc = tsv[m];
                 }
             }
-        }
+        };
+        window(IntC<TW>{}, 0);
+        window(IntC<NTRIAL - TW>{}, TW);
         // The final pass at the chain's scale (after the trials scale > 0 unless the accepted trial's sum of w*x*q
         // was negative: either make_qp_quants' positive scale or an accepted one). A lane whose chain ended on a
         // negative scale keeps the accepted trial's grid points, found here again by the same searches at that
