@@ -508,12 +508,15 @@ DEV float iq2_16_search(const float (&x)[16], const float (&qv)[16], float sigma
         int tacc = -1;
         float acc_id = 0.f, acc_sc = 0.f;
         unsigned acc_og = 3u;
-#pragma unroll 1
-        for (int w0 = 0; w0 < NT; w0 += TW) {
-            float idv[TW], tsv[TW], sqx[TW], sq2[TW];
+        // (a window of W trials from trial w0: two of TW, then one of the NT - 2 TW left, so that no walk evaluates a
+        // trial past the last)
+        auto window = [&](auto wc, int w0) {
+            constexpr int W = decltype(wc)::value;
+            FiltWS<W> &fw = *(FiltWS<W> *)&fws;
+            float idv[W], tsv[W], sqx[W], sq2[W];
             unsigned valid = 0;
 #pragma unroll
-            for (int m = 0; m < TW; ++m) {
+            for (int m = 0; m < W; ++m) {
                 idv[m] = (5 + (w0 + m - 9) * 0.1f) / mx;
                 tsv[m] = 1 / idv[m];
                 sqx[m] = sq2[m] = 0.f;
@@ -528,13 +531,13 @@ DEV float iq2_16_search(const float (&x)[16], const float (&qv)[16], float sigma
                     xk[i] = xval[8 * k + i];
                     wk[i] = waux[8 * k + i];
                 }
-                int gk[TW];
-                window_group<TW, 9, 512>(xk, wk, idv, tsv, valid, map3, p, grid, fws, ws1, wsm, gk, ogk[k]);
+                int gk[W];
+                window_group<W, 9, 512>(xk, wk, idv, tsv, valid, map3, p, grid, fw, ws1, wsm, gk, ogk[k]);
 #pragma unroll
-                for (int m = 0; m < TW; ++m) sums_q8(weight + 8 * k, xval + 8 * k, grid[gk[m]], sqx[m], sq2[m]);
+                for (int m = 0; m < W; ++m) sums_q8(weight + 8 * k, xval + 8 * k, grid[gk[m]], sqx[m], sq2[m]);
             }
 #pragma unroll
-            for (int m = 0; m < TW; ++m) {
+            for (int m = 0; m < W; ++m) {
                 if (w0 + m < NT && live && sq2[m] > 0 && sqx[m] * sqx[m] > best * sq2[m]) {
                     scale = sqx[m] / sq2[m];
                     best = scale * sqx[m];
@@ -544,7 +547,11 @@ DEV float iq2_16_search(const float (&x)[16], const float (&qv)[16], float sigma
                     acc_og = ((ogk[0] >> m) & 1u) | (((ogk[1] >> m) & 1u) << 1);
                 }
             }
-        }
+        };
+        static_assert(NT > 2 * TW && NT <= 3 * TW, "windows: two of TW and the rest");
+#pragma unroll 1
+        for (int w0 = 0; w0 < 2 * TW; w0 += TW) window(IntC<TW>{}, w0);
+        window(IntC<NT - 2 * TW>{}, 2 * TW);
         on_grid[0] = (acc_og & 1u) != 0;
         on_grid[1] = (acc_og & 2u) != 0;
         // (a group left at levels 0 is on the grid: on_grid stays true for it)
