@@ -30,7 +30,9 @@ extern "C" {
  * no records returns 0 (the k-quants, Q8_0 and IQ4 need no tables). A file that carries the stand-in mark (a record
  * of type 0x53594e54, written by this package's table generator, never by ggml's) loads its IQ1/IQ2/IQ3 tables only
  * when the environment sets GPUQ_ALLOW_SYNTHETIC_TABLES=1; otherwise it returns 0 with those types unavailable
- * (gpuq_can_quantize / gpuq_can_dequantize_type report 0), since their grid indices would not be ggml's. */
+ * (gpuq_can_quantize / gpuq_can_dequantize_type report 0), since their grid indices would not be ggml's. A second
+ * call replaces the tables for later calls and keeps the earlier ones allocated until the process ends (graphs
+ * captured before it go on reading them); it must not overlap calls from other threads. */
 int gpuq_init(const char *tables_path, int device);
 
 /* gpuq/gpuq.hip:2082 gpuq_block_bytes: bytes of one block of the type, 0 for an unknown type */
@@ -91,7 +93,8 @@ size_t gpuq_requantize_dev(int src_type, const void *d_raw, int type, void *d_ds
  * oracle computes the same ones). Types: the i-quants with a dequantizer grid, IQ4_XS and Q2_K..Q6_K. Asynchronous
  * on `stream` (part of each update runs on an internal stream that is joined back into `stream` before the call
  * returns). Calls share one library scratch buffer; each call's launches wait for the previous call's, on whatever
- * stream that one ran, so calls from several streams are ordered on the device. */
+ * stream that one ran, so calls from several streams are ordered on the device. Refused (returns 0 before any
+ * launch) on a stream under capture: graphs use gpuq_ldlq_dev_noalloc. */
 size_t gpuq_ldlq_dev(int type, float *d_wp, const double *d_u, int64_t u_stride, const float *d_qw, int64_t nmat,
                      int64_t ne1, int64_t ne0, const int64_t *blk_order, int feedback, void *d_out, void *stream);
 

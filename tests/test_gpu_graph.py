@@ -66,3 +66,51 @@ def test_graph_replays_match_eager(oracle_lib, typ):
             assert np.array_equal(got, want[i]), "replay %d input %d: %d bytes differ" % (rep, i,
                                                                                           int((got != want[i]).sum()))
     assert gq.gpuq_take_error() == 0
+
+
+@pytest.mark.gpu
+def test_graph_replays_beside_eager_launches_on_another_stream(oracle_lib):
+    """A captured launch keeps its tile counter for good, so it takes a slot that eager launches never reuse: replays
+    on one stream overlap more eager launches (on a second stream) than the eager slots, and both give their own
+    inputs' bytes."""
+    import torch
+    torch.cuda.init()
+    import gpuq
+    gq = gpuq.load_gpuq(0)
+    typ = 16
+    xs, im = inputs(seed=23, nrow=8)
+    nrow, ncol = xs[0].shape
+    nb = nrow * gpuq.row_bytes(gq, typ, ncol)
+    d_im = torch.from_numpy(im).cuda()
+    d_xg, d_xe = torch.from_numpy(xs[0]).cuda(), torch.from_numpy(xs[1]).cuda()
+    d_og, d_oe = torch.zeros(nb, dtype=torch.uint8, device="cuda"), torch.zeros(nb, dtype=torch.uint8, device="cuda")
+
+    def launch(x, out):
+        return gq.gpuq_requantize_dev(F32, x.data_ptr(), typ, out.data_ptr(), 1, nrow, ncol, d_im.data_ptr(),
+                                      torch.cuda.current_stream().cuda_stream)
+
+    want_g = oracle_lib.quantize(typ, xs[0], im).reshape(-1)
+    want_e = oracle_lib.quantize(typ, xs[1], im).reshape(-1)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        assert launch(d_xg, d_og) == nb
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    print("case graph beside eager: capture", flush=True)
+    with torch.cuda.graph(g):
+        assert launch(d_xg, d_og) == nb
+    torch.cuda.synchronize()
+    eager = torch.cuda.Stream()
+    n_eager = 4096 + 512                              # more than the eager slots: every eager slot is reused
+    print("case graph beside eager: %d eager launches, replays every 256" % n_eager, flush=True)
+    for i in range(n_eager):
+        with torch.cuda.stream(eager):
+            assert launch(d_xe, d_oe) == nb
+        if i % 256 == 0:
+            g.replay()
+    torch.cuda.synchronize()
+    assert np.array_equal(d_og.cpu().numpy(), want_g)
+    assert np.array_equal(d_oe.cpu().numpy(), want_e)
+    assert gq.gpuq_take_error() == 0

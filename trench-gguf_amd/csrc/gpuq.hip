@@ -38,10 +38,13 @@ extern "C" size_t gpuq_block_bytes(int type);
 static constexpr int64_t LDLQ_SCRATCH_ROWS = 8192;
 static __device__ __align__(256) double scratch[2 * LDLQ_SCRATCH_ROWS * 256];
 
-// The quantize launches' tile counters (the tile queue of k_quant): each launch takes the next of TILE_SLOTS slots
-// and zeroes it on its stream before the kernel, so launches in flight at once on any streams use distinct counters
-// while there are at most TILE_SLOTS of them. Addresses taken per device at gpuq_init, as for `scratch`.
-static constexpr unsigned TILE_SLOTS = 4096;
+// The quantize launches' tile counters (the tile queue of k_quant), zeroed by a kernel on the launch's stream before
+// the quantize kernel. Eager launches cycle through the first TILE_EAGER slots, so launches in flight at once on any
+// streams use distinct counters while there are at most TILE_EAGER of them. A launch recorded under stream capture
+// keeps its slot in the graph for good, so each takes one of the other TILE_SLOTS - TILE_EAGER slots, never handed
+// out again (eager launches cannot alias a graph's counter; once they are used up a captured launch fails). Addresses
+// taken per device at gpuq_init, as for `scratch`.
+static constexpr unsigned TILE_SLOTS = 16384, TILE_EAGER = 4096;
 static __device__ __align__(256) unsigned long long tile_ctr[TILE_SLOTS];
 
 __global__ void k_tile_reset(unsigned long long *ctr) {
@@ -52,7 +55,8 @@ namespace {
 
 double *g_scratch[64] = {};    // per device: the device address of `scratch`
 unsigned long long *g_tile_ctr[64] = {};   // per device: the device address of `tile_ctr`
-std::atomic<unsigned> g_tile_slot{0};
+std::atomic<unsigned> g_tile_slot{0};      // eager launches: the next slot (mod TILE_EAGER)
+std::atomic<unsigned> g_tile_graph{0};     // captured launches: slots TILE_EAGER + n taken so far
 
 struct Tabs {
     bool ok = false;
@@ -66,6 +70,7 @@ struct Tabs {
 };
 
 Tabs g_tabs[64];
+std::vector<void *> g_retired;  // device tables replaced by a later gpuq_init (never freed: see gpuq_init)
 // the record type that marks a table file holding stand-in codebooks instead of ggml's (the build's own generator
 // writes it; a file written from ggml by the reference's gpuq_tables.c has none)
 constexpr int SYNTHETIC_MARK = 0x53594e54;
@@ -219,7 +224,22 @@ template <class T, int SRC> bool launch_q(const QParams &p0, hipStream_t st) {
             occ.store(n);
         }
         cap = (int64_t)g_ncu * n;
-        p.tiles = g_tile_ctr[g_device] + g_tile_slot.fetch_add(1) % TILE_SLOTS;
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cs) != hipSuccess) return false;
+        unsigned slot;
+        if (cs == hipStreamCaptureStatusNone) {
+            slot = g_tile_slot.fetch_add(1) % TILE_EAGER;
+        } else {
+            const unsigned c = g_tile_graph.fetch_add(1);
+            if (cs != hipStreamCaptureStatusActive || c >= TILE_SLOTS - TILE_EAGER) {
+                if (cs == hipStreamCaptureStatusActive)
+                    fprintf(stderr, "gpuq: the %u tile counters reserved for captured launches are used up\n",
+                            TILE_SLOTS - TILE_EAGER);
+                return false;
+            }
+            slot = TILE_EAGER + c;
+        }
+        p.tiles = g_tile_ctr[g_device] + slot;
     }
     if (wgs > cap) wgs = cap;
     if (wgs < 1) wgs = 1;
@@ -638,11 +658,11 @@ extern "C" int gpuq_init(const char *tables, int device) {
             if (!pack_search(r.type, r.map, r.neigh, r.m3, r.nb)) return 6;
         }
     }
-    // the tables of an earlier call are replaced (once no launch can read them any more)
-    if (hipDeviceSynchronize() != hipSuccess) return 4;
+    // the tables of an earlier call are replaced but stay allocated until the process ends: launches still in flight
+    // and graphs captured before this call keep the old pointers in their parameters and go on reading them
     for (Tabs &t : g_tabs) {
         for (void *p : {(void *)t.grid, (void *)t.map, (void *)t.map3, (void *)t.neigh, (void *)t.dq})
-            if (p) (void)hipFree(p);
+            if (p) g_retired.push_back(p);
         t = Tabs();
     }
     // stand-in codebooks (the file carries the mark) are loaded only where the caller asks for them: quantizing
@@ -882,6 +902,14 @@ extern "C" size_t gpuq_ldlq_dev(int type, float *d_wp, const double *d_u, int64_
     if (!ldlq_args_ok(type, d_wp, d_u, u_stride, d_qw, nmat, ne1, ne0, blk_order, d_out)) return 0;
     const hipStream_t st = (hipStream_t)stream;
     const int64_t nblk = ne0 / QK, bb = (int64_t)gpuq_block_bytes(type), rows = nmat * ne1;
+    // not capturable: its Es buffer grows, it is shared with eager calls through an event that a capture would only
+    // record as a node, and it forks onto the library's side stream; under capture, gpuq_ldlq_dev_noalloc
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess) return 0;
+    if (cs != hipStreamCaptureStatusNone) {
+        fprintf(stderr, "gpuq_ldlq_dev: refused under stream capture (use gpuq_ldlq_dev_noalloc)\n");
+        return 0;
+    }
     std::lock_guard<std::mutex> lock(g_mu);
     const bool fb = feedback && nblk > 1;
     if (fb && (!g_es.grow((size_t)2 * rows * QK * 8) || !side_stream_ready())) return 0;
