@@ -6,7 +6,8 @@
 One "step" is one pass of the quantizer over one workload tensor already resident in HBM (the device entry point
 gpuq_requantize_dev: source bytes decoded in registers, quantized, blocks written to HBM). The headline line is
 IQ2_XXS with imatrix on 256 stacked BF16 experts of 2048 x 7168 (expert e ~ N(0, s_e), s_e ~ U[0.01, 0.03], a
-log-normal(0, 1.5) imatrix a expert). `per_type` adds Q8_0 on a 4096 x 4096 F32 tensor, Q4_K and Q6_K on a
+log-normal(0, 1.5) imatrix a expert). `per_type` adds Q8_0 on a 4096 x 4096 F32 tensor (and on 64 of them, 4.3 GB, where launch
+and ramp time no longer weigh), Q4_K and Q6_K on a
 2048 x 7168 BF16 tensor (N(0, 0.02) plus 0.1% outliers at +-8 sigma, a log-normal imatrix), IQ1_S / IQ1_M on 384 x
 2048 x 7168 MXFP4 experts and IQ2_S with LDLQ error feedback on 64 BF16 experts; `other_types` the remaining nine
 types on the 2048 x 7168 tensor (GPU rate, roofline, byte spot check on 64 rows). Kernel time comes from HIP events
@@ -43,7 +44,7 @@ VALU_PEAK_TOPS = 78.6          # 157.3 TFLOP/s FP32 vector / 2 flops an FMA: 2 w
 FP64_PEAK_TFLOPS = 78.6        # MI355X FP64 (vector and matrix)
 MALL_BYTES = 256 << 20         # Infinity Cache
 CPU_MIN_S = 10.0               # the CPU baseline repeats its sample until this much CPU time has run
-ENTRIES = ["IQ2_XXS", "Q8_0", "Q4_K", "Q6_K", "IQ1_S", "IQ1_M", "LDLQ", "other"]
+ENTRIES = ["IQ2_XXS", "Q8_0", "Q8_0_large", "Q4_K", "Q6_K", "IQ1_S", "IQ1_M", "LDLQ", "other"]
 OTHER = ["Q2_K", "Q3_K", "Q5_K", "IQ4_NL", "IQ4_XS", "IQ2_XS", "IQ2_S", "IQ3_XXS", "IQ3_S"]
 
 
@@ -119,6 +120,16 @@ def wl_c1(torch, gpuq):
     g = torch.Generator(device="cuda").manual_seed(0)
     x = make_f32(torch, g, (4096, 4096), 0.02)
     return Workload("F32 4096x4096 N(0,0.02), seed 0", "F32 4096x4096", gpuq.F32, 1, 4096, 4096, x, None)
+
+
+def wl_q8_large(torch, gpuq, nmat=64):
+    """Q8_0's streaming rate away from launch and ramp time: nmat F32 matrices of 4096 x 4096 (4.3 GB at 64)"""
+    g = torch.Generator(device="cuda").manual_seed(4)
+    x = torch.empty((nmat, 4096, 4096), dtype=torch.float32, device="cuda")
+    for e in range(0, nmat, 8):
+        x[e:e + 8] = torch.randn((min(8, nmat - e), 4096, 4096), device="cuda", generator=g) * 0.02
+    return Workload("F32 %dx4096x4096 N(0,0.02), seed 4" % nmat, "F32 %dx4096x4096" % nmat, gpuq.F32, nmat, 4096,
+                    4096, x.reshape(-1), None)
 
 
 def wl_c2(torch, gpuq):
@@ -550,6 +561,13 @@ def main():
         per["Q8_0"], _ = type_entry(torch, gq, gpuq, orc, orc_ops, c1, gpuq.Q8_0, args.steps, args.warmup, c1.nrow,
                                     want_cpu)
         del c1
+    if want("Q8_0_large"):
+        ql = wl_q8_large(torch, gpuq)
+        log("per type: Q8_0 on %s (the streaming rate at a size launch time does not weigh on)" % ql.name)
+        per["Q8_0_large"], _ = type_entry(torch, gq, gpuq, orc, orc_ops, ql, gpuq.Q8_0, args.steps, args.warmup,
+                                          64, False)
+        del ql
+        torch.cuda.empty_cache()
     c2 = None
     if want("Q4_K") or want("Q6_K") or any(want(t) for t in OTHER) or want("other"):
         c2 = wl_c2(torch, gpuq)

@@ -1509,7 +1509,10 @@ static float affine_levels(int with_im, int n, int nmax, const float *x, const f
             sum_xl += w * l * x[i];
         }
         const float D = sum_w * sum_l2 - sum_l * sum_l;
-        OPS(5 + C_DIV + n * 13 + 4);
+        /* a level with the imatrix rule: x - mn, the product, one clamp to [0, nmax] (NaN to 0) and the rounding
+         * of a value in [0, nmax] as two float adds (exact there); the plain rule's ggml rounding of an unbounded
+         * value is the integer nearest_int plus the clamp and a conversion; then the three sums (6) */
+        OPS(5 + C_DIV + n * (with_im ? 11 : 13) + 4);
         if (!(D > 0)) continue;
         float this_scale = (sum_w * sum_xl - sum_x * sum_l) / D;
         float this_min = (sum_l2 * sum_x - sum_l * sum_xl) / D;
@@ -1526,7 +1529,7 @@ static float affine_levels(int with_im, int n, int nmax, const float *x, const f
             const float w = with_im ? kw(weights, x, i) : weights[i];
             err += w * diff;
         }
-        OPS(n * 7 + 1);
+        OPS(n * (with_im ? 6 : 7) + 1);     /* (the imatrix rule's levels are floats already: no conversion) */
         if (err < best) {
             for (int i = 0; i < n; ++i) L[i] = Laux[i];
             best = err;

@@ -1,17 +1,19 @@
-// trench-gguf_amd/csrc/filter.cuh - the filtered neighbour search of IQ2_XXS: one walk of a neighbour list serves
-// every trial scale whose key (and so whose list) is the same.
+// trench-gguf_amd/csrc/filter.cuh - the filtered neighbour search of IQ2_XXS / IQ2_XS: one walk of a neighbour list
+// serves every trial scale whose key (and so whose list) is the same.
 //
 // The trial scales of a group mostly round to the same key: over IQ2_XXS's 13 trials a group's key changes about
 // twice, so ggml's serial scan (gpuq/gpuq.hip:178-197) walks the same list about five times at different scales.
 // Here a list is walked once for all the consecutive trials of a window that share it. A candidate's distance at
 // scale s, d2(s) = sum_i w_i (s q_i - x_i)^2, is split as s^2 A - 2 s B + C with A = sum w q^2, B = sum (w x) q (once
-// a candidate) and C = sum (w x) x (once a list), so each further trial costs a few operations instead of ggml's 40.
-// That value only approximates the distance ggml computes (its own operation order, fp32 roundings); the search
-// uses it to rule candidates out, never to pick one that ggml would not:
+// a candidate) and C = sum (w x) x (once a list), and evaluated as D = fma(s, fma(s, A, B'), C) with B' the fma chain
+// of the products of -2 (w x) and q (the factor -2 is exact), two operations a trial instead of ggml's 40. That value
+// only approximates the distance ggml computes (its own operation order, fp32 roundings); the search uses it to rule
+// candidates out, never to pick one that ggml would not:
 //
 //   with w >= 0, s > 0, q in 1..7 and S = sum w (s q + |x|)^2, ggml's d2 lies within 13.3 u S of the exact sum
-//   (u = 2^-24; its products and sums in fp32) and so does the approximation D (11.1 u S: the fma chains of A, B, C
-//   and D; intermediates below the normal range add at most 2^-149 each, which the lower limit on Smax below makes
+//   (u = 2^-24; its products and sums in fp32) and so does D (the fma chains of A, B' and C are within 8u, 9u and
+//   9u of their terms' magnitudes, and the two fmas of the trial add u each: at most 11 u S to first order, 11.1 u S
+//   in all; intermediates below the normal range add at most 2^-149 each, which the lower limit on Smax below makes
 //   negligible), and S <= Smax = s^2 49 sum(w) + 14 s sum(w |x|) + sum(w x^2) for every candidate; so with
 //   delta = 2^-19 Smax >= 24.4 u S / 0.76 (the slack covers Smax's own rounding), the candidate of least D is ggml's
 //   pick whenever every other candidate's D exceeds it by more than 2 delta: each of their ggml distances is then
@@ -29,11 +31,11 @@
 
 // per-wave workspace of the search over windows of W trials. List m of lane L (id e = m*64 + L) is the run of the
 // lane's trials m .. m+ntr-1 that share one key. Each lane stages what a walker needs of its lists, as planes of
-// float4 (the 64 lanes' writes of one plane are consecutive): w*x (2 planes), w (2), then C = sum (w x) x, the
-// trials' s^2 and -2s (W each).
+// float4 (the 64 lanes' writes of one plane are consecutive): -2 w*x (2 planes), w (2), then C = sum (w x) x and the
+// trials' scales s (W).
 template <int W> struct FiltWS {
     static_assert(W >= 1 && W <= 7, "trials a window: 1..7 (list ids < 512, run lengths < 8)");
-    static constexpr int NPL = 4 + (1 + 2 * W + 3) / 4;
+    static constexpr int NPL = 4 + (1 + W + 3) / 4;
     float4 own[NPL][64];
     int2 ent[64 * W];               // first point's offset | length << 21, next list with candidates | e << 9 | ntr << 18
     unsigned k1[W][64], k2[W][64];  // per trial and lane: the least and the second-least key of the trial's list
@@ -55,7 +57,7 @@ DEV unsigned umed3(unsigned a, unsigned b, unsigned c) {
 // The deal: each list is cut into pieces of CH consecutive candidates, the wave's pieces are concatenated lane by
 // lane, list by list (a wave prefix sum), and walker L takes the contiguous run of R = ceil(pieces / 64) pieces from
 // L*R, one a round. A walker changes lists only between rounds, so the walkers' list changes (merge the running
-// pairs, read the new owner's values) come once a round rather than at any position, and within a round every walker
+// keys, read the new owner's values) come once a round rather than at any position, and within a round every walker
 // evaluates CH candidates of one list (positions past the list's end are masked). The next piece's list entries are
 // read while the current piece is evaluated.
 template <int W, int IB, int NG, int CH = 4>
@@ -84,18 +86,16 @@ DEV void coop_filter(const int (&cnt)[W], const int (&off)[W], const int (&ntr)[
         float C = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            v[i] = wv[i] * xv[i];
+            const float wx = wv[i] * xv[i];
+            v[i] = -2.f * wx;
             v[8 + i] = wv[i];
-            C = fmaf(v[i], xv[i], C);
+            C = fmaf(wx, xv[i], C);
         }
         v[16] = C;
 #pragma unroll
-        for (int t = 0; t < W; ++t) {
-            v[17 + t] = s[t] * s[t];
-            v[17 + W + t] = -2.f * s[t];
-        }
+        for (int t = 0; t < W; ++t) v[17 + t] = s[t];
 #pragma unroll
-        for (int i = 17 + 2 * W; i < NPL * 4; ++i) v[i] = 0.f;
+        for (int i = 17 + W; i < NPL * 4; ++i) v[i] = 0.f;
 #pragma unroll
         for (int pl = 0; pl < NPL; ++pl)
             ws.own[pl][lane] = make_float4(v[4 * pl], v[4 * pl + 1], v[4 * pl + 2], v[4 * pl + 3]);
@@ -153,18 +153,21 @@ DEV void coop_filter(const int (&cnt)[W], const int (&off)[W], const int (&ntr)[
     }
     // evaluation state: the list (id, first trial, trials), its owner's values, the walker's two least keys a trial
     int cur = -1, cm = 0, cn = 0;
-    float wx[8], w[8], C, s2[W], m2s[W];
+    float nwx[8], w[8], C, sc[W];
     unsigned r1[W], r2[W];
 #pragma unroll
     for (int t = 0; t < W; ++t) r1[t] = r2[t] = ~0u;
-    auto flush = [&]() {   // the walker's pairs into the list's pairs, for the list's trials
+    // the walker's pairs into the list's pairs, for the list's trials (a trial outside them offers ~0u, which changes
+    // nothing): the first slots' atomics all issued, then the second slots' (no branch a trial, so the atomics of the
+    // trials overlap instead of waiting one after another)
+    auto flush = [&]() {
+        unsigned o[W];
 #pragma unroll
-        for (int t = 0; t < W; ++t) {
-            if ((unsigned)(t - cm) < (unsigned)cn) {
-                const unsigned old = atomicMin(&ws.k1[t][cur & 63], r1[t]);
-                atomicMin(&ws.k2[t][cur & 63], umed3(old, r1[t], r2[t]));   // the second least of the four
-            }
-        }
+        for (int t = 0; t < W; ++t)
+            o[t] = atomicMin(&ws.k1[t][cur & 63], (unsigned)(t - cm) < (unsigned)cn ? r1[t] : ~0u);
+#pragma unroll
+        for (int t = 0; t < W; ++t)   // (the second least of the slot's old key and the walker's two)
+            atomicMin(&ws.k2[t][cur & 63], (unsigned)(t - cm) < (unsigned)cn ? umed3(o[t], r1[t], r2[t]) : ~0u);
     };
     int idx[CH];
 #pragma unroll
@@ -197,7 +200,7 @@ DEV void coop_filter(const int (&cnt)[W], const int (&off)[W], const int (&ntr)[
 #pragma unroll
             for (int pl = 0; pl < 2; ++pl) {
                 const float4 a = ws.own[pl][ow], b = ws.own[2 + pl][ow];
-                wx[4 * pl] = a.x; wx[4 * pl + 1] = a.y; wx[4 * pl + 2] = a.z; wx[4 * pl + 3] = a.w;
+                nwx[4 * pl] = a.x; nwx[4 * pl + 1] = a.y; nwx[4 * pl + 2] = a.z; nwx[4 * pl + 3] = a.w;
                 w[4 * pl] = b.x; w[4 * pl + 1] = b.y; w[4 * pl + 2] = b.z; w[4 * pl + 3] = b.w;
             }
             float v[NPL * 4 - 16];
@@ -209,8 +212,7 @@ DEV void coop_filter(const int (&cnt)[W], const int (&off)[W], const int (&ntr)[
             C = v[0];
 #pragma unroll
             for (int t = 0; t < W; ++t) {
-                s2[t] = v[1 + t];
-                m2s[t] = v[1 + W + t];
+                sc[t] = v[1 + t];
                 r1[t] = r2[t] = ~0u;
             }
         }
@@ -227,16 +229,16 @@ DEV void coop_filter(const int (&cnt)[W], const int (&off)[W], const int (&ntr)[
 #pragma unroll
         for (int r = 0; r < CH; ++r) {
             const uint32_t lo = (uint32_t)pt[r], hi = (uint32_t)(pt[r] >> 32);
-            float A = 0.f, B = 0.f;
+            float A = 0.f, B = 0.f;                     // (B: -2 sum (w x) q)
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const float q = small_int_f((float)(((i < 4 ? lo : hi) >> (8 * (i % 4))) & 0xffu));
                 A = fmaf(w[i], q * q, A);
-                B = fmaf(wx[i], q, B);
+                B = fmaf(nwx[i], q, B);
             }
 #pragma unroll
             for (int t = 0; t < W; ++t) {
-                const float D = fmaf(s2[t], A, fmaf(m2s[t], B, C));
+                const float D = fmaf(sc[t], fmaf(sc[t], A, B), C);
                 const unsigned key = (__float_as_uint(D) & KHI) | low[r];
                 r2[t] = umed3(r1[t], r2[t], key);   // (r1 <= r2: the second least of the three)
                 r1[t] = r1[t] < key ? r1[t] : key;
