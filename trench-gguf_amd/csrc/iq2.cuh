@@ -166,11 +166,12 @@ DEV void sums_q8(const float *w, const float *xv, uint64_t pt, float &sumqx, flo
 // undecided goes through the exact search, up to 4 a lane a call (a search that accepts nothing flags the error, as
 // the reference traps, and yields 0). gk[m]: trial m's grid index (0 for a trial that does not run); og: bit m set
 // where trial m's key is on the grid (and for a trial that does not run). IB, NG: the grid indices' bits and the
-// grid's size. The staged area of fws, ws and wsm is one (the caller's workspace).
-template <int TW, int IB, int NG>
+// grid's size. The staged area of fws, ws and wsm is one (the caller's workspace). DEFER: the undecided trials are
+// not searched here but returned in undec (bit m; their gk[m] is 0), for the caller to search with others at once.
+template <int TW, int IB, int NG, bool DEFER = false>
 DEV void window_group(const float (&xk)[8], const float (&waux)[8], const float (&idv)[TW], const float (&tsv)[TW],
                       unsigned valid, const int32_t *map3, const QParams &p, const uint64_t *grid, FiltWS<TW> &fws,
-                      CoopWS &ws, CoopWSM<4> &wsm, int (&gk)[TW], unsigned &og) {
+                      CoopWS &ws, CoopWSM<4> &wsm, int (&gk)[TW], unsigned &og, unsigned &undec) {
     float sw = 0.f, swx = 0.f, swxx = 0.f;      // the filter's bound: sums of w, w|x|, w x^2
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -204,6 +205,12 @@ DEV void window_group(const float (&xk)[8], const float (&waux)[8], const float 
     for (int m = 0; m < TW; ++m) {
         gk[m] = mk[m] >= 0 ? mk[m] : filt_pick<IB>(k1[m], k2[m], tsv[m], sw, swx, swxx);
         if (gk[m] < 0) amb |= 1u << m;
+    }
+    undec = DEFER ? amb : 0u;
+    if (DEFER) {
+#pragma unroll
+        for (int m = 0; m < TW; ++m) gk[m] = gk[m] < 0 ? 0 : gk[m];
+        return;
     }
     if (__ballot(amb != 0)) coop_stage<8>(ws, xk, waux);
 #pragma unroll 1
@@ -291,30 +298,38 @@ struct KIQ2XXS : Iq8Tab<256> {
         }
         // The trials, a window of TW at a time (every lane runs them: the neighbour searches are wave-wide), group by
         // group: a group's values are staged once for the window, each trial's key on the grid is its point, and the
-        // trials that share an off-grid key are searched by one filtered walk of its list (filter.cuh); a trial the
-        // filter leaves undecided goes through the exact search. The window's trials' sums of w*x*q and w*q*q
-        // gather group by group in index order, and the acceptance chain then runs over the window in ggml's order
+        // trials that share an off-grid key are searched by one filtered walk of its list (filter.cuh). A trial the
+        // filter leaves undecided waits: after both windows the undecided searches of the whole tile go through the
+        // exact search together (two a lane a call; an exact call costs about the same for one search as for many,
+        // and a wave of 64 lanes has some undecided trial in about a third of its window-group calls). The trials'
+        // grid indices are kept a byte a group (pk[t], group k at bits 8k); then the trials' sums of w*x*q and w*q*q
+        // gather group by group in index order, and the acceptance chain runs over the 13 trials in ggml's order
         // (each trial's searches do not depend on another trial's outcome, so this order changes nothing). The
         // chain keeps the accepted trial (its number and scales), not its grid points.
         float best = 0;
         int tacc = -1;          // the last accepted trial (-1: none), its inverse scale and scale
         float acc_id = 0.f, acc_sc = 0.f;
-        // (a window of W trials from trial w0: the first of TW, the second of the NTRIAL - TW left, so that no walk
+        uint32_t pk[NTRIAL];
+        uint64_t und = 0;       // undecided searches: group k, trial t at bit 13k + t
+#pragma unroll
+        for (int t = 0; t < NTRIAL; ++t) pk[t] = 0u;
+        // trial t's inverse scale (as ggml forms it)
+        auto trial_id = [&](int t) { return (5 + (t - 6) * 0.1f) / eff_max; };
+        // (a window of W trials from trial W0: the first of TW, the second of the NTRIAL - TW left, so that no walk
         // evaluates a trial past the last)
-        auto window = [&](auto wc, int w0) {
-            constexpr int W = decltype(wc)::value;
+        auto window = [&](auto wc, auto w0c) {
+            constexpr int W = decltype(wc)::value, W0 = decltype(w0c)::value;
             FiltWS<W> &fw = *(FiltWS<W> *)&fws;
-            float idv[W], tsv[W], sqx[W], sq2[W];
+            float idv[W], tsv[W];
 #pragma unroll
             for (int m = 0; m < W; ++m) {
-                idv[m] = (5 + (w0 + m - 6) * 0.1f) / eff_max;
+                idv[m] = trial_id(W0 + m);
                 tsv[m] = 1 / idv[m];
-                sqx[m] = sq2[m] = 0.f;
             }
             unsigned valid = 0;
 #pragma unroll
             for (int m = 0; m < W; ++m)
-                if (live && w0 + m < NTRIAL) valid |= 1u << m;
+                if (live && W0 + m < NTRIAL) valid |= 1u << m;
 #pragma unroll 1
             for (int k = 0; k < 4; ++k) {       // (not unrolled: one copy of the search code, groups kept apart)
                 float xk[8], waux[8];           // group k: rotated to the front (rot8 below)
@@ -324,27 +339,82 @@ struct KIQ2XXS : Iq8Tab<256> {
                     waux[i] = sqrtf(weight[i]);
                 }
                 int gk[W];                     // the trials' grid indices of group k
-                unsigned og;
-                window_group<W, 8, 256>(xk, waux, idv, tsv, valid, map3, p, grid, fw, ws, wsm, gk, og);
+                unsigned og, undec;
+                window_group<W, 8, 256, true>(xk, waux, idv, tsv, valid, map3, p, grid, fw, ws, wsm, gk, og, undec);
 #pragma unroll
-                for (int m = 0; m < W; ++m) sums_q8(weight, xval, grid[gk[m]], sqx[m], sq2[m]);
+                for (int m = 0; m < W; ++m) pk[W0 + m] |= (uint32_t)gk[m] << (8 * k);
+                und |= (uint64_t)undec << (13 * k + W0);
                 rot8(xval);
                 rot8(weight);
             }
-            // the acceptance chain over the window's trials, in ggml's order
+        };
+        window(IntC<TW>{}, IntC<0>{});
+        window(IntC<NTRIAL - TW>{}, IntC<TW>{});
+        // the undecided searches, two a lane a call (each list with its group's values staged in its own row)
+#pragma unroll 1
+        while (__ballot(und != 0)) {
+            int kk[2], tt[2], cnt[2], off[2], gi[2];
+            float sc[2];
 #pragma unroll
-            for (int m = 0; m < W; ++m) {
-                if (w0 + m < NTRIAL && live && sq2[m] > 0 && sqx[m] * sqx[m] > best * sq2[m]) {
-                    scale = sqx[m] / sq2[m];
-                    best = scale * sqx[m];
-                    tacc = w0 + m;
-                    acc_id = idv[m];
-                    acc_sc = tsv[m];
+            for (int j = 0; j < 2; ++j) {
+                const int b = und ? __builtin_ctzll(und) : -1;
+                und &= und - 1;
+                kk[j] = b < 0 ? 0 : b / 13;
+                tt[j] = b < 0 ? 0 : b - 13 * kk[j];
+                float xs[8], wa[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    xs[i] = kk[j] == 0 ? xval[i] : kk[j] == 1 ? xval[8 + i] : kk[j] == 2 ? xval[16 + i] : xval[24 + i];
+                    wa[i] = sqrtf(kk[j] == 0 ? weight[i] : kk[j] == 1 ? weight[8 + i] : kk[j] == 2 ? weight[16 + i]
+                                                                                                  : weight[24 + i]);
+                }
+                const float id = trial_id(tt[j]);
+                sc[j] = 1 / id;
+                const int mv = b < 0 ? 0 : map3[group_key3(xs, id)];
+                cnt[j] = b < 0 ? 0 : m3_cnt(mv);
+                off[j] = b < 0 ? 0 : m3_off(mv);
+                coop_stage<8>(ws2, xs, wa, j * 64 + lane_id());
+            }
+            coop_search_m<2, 4>(cnt, off, sc, p.neigh, p.neigh_len, ws2, EvalIq8{grid}, gi);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                if (cnt[j] > 0) {
+                    int gv = gi[j];
+                    if (gv < 0) {
+                        flag_err(p);
+                        gv = 0;
+                    }
+#pragma unroll
+                    for (int t = 0; t < NTRIAL; ++t)
+                        if (t == tt[j]) pk[t] |= (uint32_t)gv << (8 * kk[j]);
                 }
             }
-        };
-        window(IntC<TW>{}, 0);
-        window(IntC<NTRIAL - TW>{}, TW);
+        }
+        {
+            float sqx[NTRIAL], sq2[NTRIAL];
+#pragma unroll
+            for (int t = 0; t < NTRIAL; ++t) sqx[t] = sq2[t] = 0.f;
+#pragma unroll 1
+            for (int k = 0; k < 4; ++k) {       // group by group, in index order (group k rotated to the front)
+#pragma unroll
+                for (int t = 0; t < NTRIAL; ++t) sums_q8(weight, xval, grid[(pk[t] >> (8 * k)) & 255u], sqx[t], sq2[t]);
+                rot8(xval);
+                rot8(weight);
+            }
+            // the acceptance chain over the trials, in ggml's order
+#pragma unroll
+            for (int t = 0; t < NTRIAL; ++t) {
+                if (live && sq2[t] > 0 && sqx[t] * sqx[t] > best * sq2[t]) {
+                    scale = sqx[t] / sq2[t];
+                    best = scale * sqx[t];
+                    tacc = t;
+                }
+            }
+        }
+        if (tacc >= 0) {
+            acc_id = trial_id(tacc);
+            acc_sc = 1 / acc_id;
+        }
         // The final pass at the chain's scale (after the trials scale > 0 unless the accepted trial's sum of w*x*q
         // was negative: either make_qp_quants' positive scale or an accepted one). A lane whose chain ended on a
         // negative scale keeps the accepted trial's grid points, found here again by the same searches at that
@@ -532,7 +602,8 @@ DEV float iq2_16_search(const float (&x)[16], const float (&qv)[16], float sigma
                     wk[i] = waux[8 * k + i];
                 }
                 int gk[W];
-                window_group<W, 9, 512>(xk, wk, idv, tsv, valid, map3, p, grid, fw, ws1, wsm, gk, ogk[k]);
+                unsigned undec;
+                window_group<W, 9, 512>(xk, wk, idv, tsv, valid, map3, p, grid, fw, ws1, wsm, gk, ogk[k], undec);
 #pragma unroll
                 for (int m = 0; m < W; ++m) sums_q8(weight + 8 * k, xval + 8 * k, grid[gk[m]], sqx[m], sq2[m]);
             }
