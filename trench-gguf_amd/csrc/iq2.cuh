@@ -567,10 +567,10 @@ DEV float iq2_16_search(const float (&x)[16], const float (&qv)[16], float sigma
     bool on_grid[2] = {true, true};
     if constexpr (GRID == 512) {
         // IQ2_XS (two-shell lists, 12.9 points on average): the 19 trials in windows of TW, group by group, through
-        // the filtered search (window_group), and the acceptance chain over each window from the trials' running
-        // sums; the chain keeps the accepted trial (number, scales, which groups were on the grid), and the pass
-        // below finds its points again: on the grid from their keys, off the grid by the same searches (IQ2_XXS's
-        // scheme, KIQ2XXS::quant)
+        // the filtered search (window_group; the trials it leaves undecided searched once a window, after both
+        // groups' walks), and the acceptance chain over each window from the trials' sums; the chain keeps the
+        // accepted trial (number, scales, which groups were on the grid), and the pass below finds its points again:
+        // on the grid from their keys, off the grid by the same searches (IQ2_XXS's scheme, KIQ2XXS::quant)
         constexpr int TW = IQ2XS_TW, NT = 19;
         FiltWS<TW> &fws = *(FiltWS<TW> *)&ws;
         CoopWS &ws1 = *(CoopWS *)&ws;
@@ -592,7 +592,12 @@ DEV float iq2_16_search(const float (&x)[16], const float (&qv)[16], float sigma
                 sqx[m] = sq2[m] = 0.f;
                 if (live && w0 + m < NT) valid |= 1u << m;
             }
-            unsigned ogk[2];
+            // the window's grid indices, group k at bits 9k; the trials the filter leaves undecided (group k, trial
+            // m at bit 8k + m) are searched after both groups' walks, four a lane a call (two of each group)
+            unsigned ogk[2], und = 0;
+            uint32_t pk[W];
+#pragma unroll
+            for (int m = 0; m < W; ++m) pk[m] = 0u;
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
                 float xk[8], wk[8];
@@ -603,9 +608,60 @@ DEV float iq2_16_search(const float (&x)[16], const float (&qv)[16], float sigma
                 }
                 int gk[W];
                 unsigned undec;
-                window_group<W, 9, 512>(xk, wk, idv, tsv, valid, map3, p, grid, fw, ws1, wsm, gk, ogk[k], undec);
+                window_group<W, 9, 512, true>(xk, wk, idv, tsv, valid, map3, p, grid, fw, ws1, wsm, gk, ogk[k],
+                                              undec);
 #pragma unroll
-                for (int m = 0; m < W; ++m) sums_q8(weight + 8 * k, xval + 8 * k, grid[gk[m]], sqx[m], sq2[m]);
+                for (int m = 0; m < W; ++m) pk[m] |= (uint32_t)gk[m] << (9 * k);
+                und |= undec << (8 * k);
+            }
+            if (__ballot(und != 0)) {
+#pragma unroll
+                for (int k = 0; k < 2; ++k) coop_stage<8>(ws, xval + 8 * k, waux + 8 * k, k * 64 + lane_id());
+            }
+#pragma unroll 1
+            while (__ballot(und != 0)) {
+                int cnt[4], off[4], gi[4], tm[4];
+                float sc[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {           // list j searches for group j & 1 (its staged row)
+                    const int k = j & 1;
+                    const unsigned u = (und >> (8 * k)) & 0xffu;
+                    const int m = u ? __builtin_ctz(u) : -1;
+                    if (m >= 0) und &= ~(1u << (8 * k + m));
+                    tm[j] = m;
+                    float id = idv[0];
+                    sc[j] = tsv[0];
+#pragma unroll
+                    for (int mm = 0; mm < W; ++mm) {
+                        if (mm == m) {
+                            id = idv[mm];
+                            sc[j] = tsv[mm];
+                        }
+                    }
+                    const int mv = m < 0 ? 0 : map3[group_key3(xval + 8 * k, id)];
+                    cnt[j] = m < 0 ? 0 : m3_cnt(mv);
+                    off[j] = m < 0 ? 0 : m3_off(mv);
+                }
+                coop_search_m<4, ch16<GRID>()>(cnt, off, sc, p.neigh, p.neigh_len, ws, EvalIq8{grid}, gi);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (cnt[j] > 0) {
+                        int gv = gi[j];
+                        if (gv < 0) {
+                            flag_err(p);
+                            gv = 0;
+                        }
+#pragma unroll
+                        for (int mm = 0; mm < W; ++mm)
+                            if (mm == tm[j]) pk[mm] |= (uint32_t)gv << (9 * (j & 1));
+                    }
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+#pragma unroll
+                for (int m = 0; m < W; ++m)
+                    sums_q8(weight + 8 * k, xval + 8 * k, grid[(pk[m] >> (9 * k)) & 511u], sqx[m], sq2[m]);
             }
 #pragma unroll
             for (int m = 0; m < W; ++m) {
