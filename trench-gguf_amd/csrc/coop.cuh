@@ -32,21 +32,26 @@
 // NP = 1 (PL = false) when the lane's M lists search for one group (row L), NP = M (PL = true) for M groups of the
 // lane (row e), or a divisor of M for M/NP searches of NP groups each (list m uses group m mod NP). A row holds SW
 // floats: NV x's then NV weights (SW = 2 NV), stored as SW/4 planes of float4 so that the lanes' staging writes are
-// consecutive too.
-template <int M, int SW = 16, bool PL = false, int NP = (PL ? M : 1)> struct CoopWSM {
-    static_assert(M == 1 || M == 2 || M == 4, "lists a lane: 1, 2 or 4");
+// consecutive too. The lists' scales are kept in ES rows a lane: ES = M (one a list), or a divisor of M when the
+// lists come in runs of M/ES with one scale (list m's scale row: m / (M / ES)). List ids take LB bits (8 up to 4 lists
+// a lane, 9 up to 8).
+template <int M, int SW = 16, bool PL = false, int NP = (PL ? M : 1), int ES = M> struct CoopWSM {
+    static_assert(M == 1 || M == 2 || M == 4 || M == 6 || M == 8, "lists a lane: 1, 2, 4, 6 or 8");
     static_assert(NP >= 1 && NP <= M && M % NP == 0, "staged rows a lane: a divisor of M");
+    static_assert(ES >= 1 && ES <= M && M % ES == 0, "scale rows a lane: a divisor of M");
     static_assert(SW == 8 || SW == 16, "staged values: 4 or 8 x's and weights");
     static constexpr int sw = SW;
     static constexpr int np = NP;
+    static constexpr int es = ES;
+    static constexpr int LB = M <= 4 ? 8 : 9;
     float4 stage[SW / 4][64 * NP];
-    int2 ent[64 * M];               // list e: first point's offset | length << 21, next list with candidates | e << 8
-    float esc[64 * M];              // list e: its scale
+    int2 ent[64 * M];               // list e: first point's offset | length << 21, next list with candidates | e << LB
+    float esc[64 * ES];             // scale row r: its lists' scale
     unsigned long long key[64 * M]; // list e: min of (distance bits << 32 | list position << 12 | grid index)
-    int mark[64];                   // walker lane: the list of its first position | position in that list << 8
+    int mark[64];                   // walker lane: the list of its first position | position in that list << LB
 };
-template <int M, int SW = 16, bool PL = false, int NP = (PL ? M : 1)> constexpr int coop_wsm_bytes() {
-    return (int)sizeof(CoopWSM<M, SW, PL, NP>);
+template <int M, int SW = 16, bool PL = false, int NP = (PL ? M : 1), int ES = M> constexpr int coop_wsm_bytes() {
+    return (int)sizeof(CoopWSM<M, SW, PL, NP, ES>);
 }
 using CoopWS = CoopWSM<1>;
 static constexpr int COOP_WS_BYTES = (int)sizeof(CoopWS);
@@ -140,13 +145,16 @@ DEV unsigned signed_key(float d) {
     return d != d ? ~0u : k;
 }
 
-template <int M, int CH = 4, bool SIGNED = false, class Eval, int SW, bool PL, int NP>
+template <int M, int CH = 4, bool SIGNED = false, class Eval, int SW, bool PL, int NP, int ES>
 DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&scale)[M], const uint16_t *neigh,
-                       int neigh_len, CoopWSM<M, SW, PL, NP> &ws, const Eval &ev, int (&gi)[M]) {
+                       int neigh_len, CoopWSM<M, SW, PL, NP, ES> &ws, const Eval &ev, int (&gi)[M]) {
     static_assert(CH == 1 || CH == 2 || CH == 4 || CH == 8, "piece size: a power of two");
     constexpr int CSH = CH == 1 ? 0 : CH == 2 ? 1 : CH == 4 ? 2 : 3;
     constexpr int ROWS = 64 * NP - 1;                   // list e's staged row: e & ROWS
     constexpr int OFF_MASK = (1 << 21) - 1;
+    constexpr int LB = CoopWSM<M, SW, PL, NP, ES>::LB, IDM = (1 << LB) - 1;
+    constexpr int SR = M / ES;                          // lists a scale row
+    auto srow = [](int e) { return SR == 1 ? e : ((e >> 6) / SR) * 64 + (e & 63); };
     // the lists through a buffer resource: 32-bit offsets, and reads past the table return 0 instead of faulting
     const __amdgpu_buffer_rsrc_t nrs = __builtin_amdgcn_make_buffer_rsrc((void *)neigh, 0, neigh_len * 2, 0x00020000);
     const int lane = lane_id();
@@ -177,8 +185,8 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
 #pragma unroll
         for (int m = M - 1; m >= 0; --m) {
             const int e = m * 64 + lane;
-            ws.ent[e] = make_int2((off[m] + 1) | (cnt[m] << 21), (carry < 0 ? e : carry) | (e << 8));
-            ws.esc[e] = scale[m];
+            ws.ent[e] = make_int2((off[m] + 1) | (cnt[m] << 21), (carry < 0 ? e : carry) | (e << LB));
+            if (SR == 1 || m % SR == 0) ws.esc[srow(e)] = scale[m];
             ws.key[e] = ~0ull;
             if (cnt[m] > 0) carry = e;
         }
@@ -188,7 +196,7 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
         int np[M];
 #pragma unroll
         for (int m = 0; m < M; ++m) np[m] = (cnt[m] + CH - 1) >> CSH;
-        deal_marks<M, 8>(ws.mark, np, incl - tot, R);
+        deal_marks<M, LB>(ws.mark, np, incl - tot, R);
     }
     wave_sync();
     const int p0 = (int)__umul24((unsigned)lane, (unsigned)R);   // this walker's first piece
@@ -196,8 +204,8 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
     int o, j;
     if (p0 < total) {
         const int mk = ws.mark[lane];
-        o = mk & 255;
-        j = mk >> 8;
+        o = mk & IDM;
+        j = mk >> LB;
     } else {                                            // (a walker with no pieces starts on the last list)
         o = wlast;
         j = 0;
@@ -208,7 +216,7 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
         const int2 oe = ws.ent[o];
         ocnt = oe.x >> 21;
         ol = oe.x & OFF_MASK;
-        nx = ws.ent[oe.y & 255];
+        nx = ws.ent[oe.y & IDM];
     }
     // evaluation state: the list being evaluated, its owner's values and scale, the best distance bits and position
     int cur = -1;
@@ -223,11 +231,11 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
         int o2 = o, j2 = j + 1, ocnt2 = ocnt, ol2 = ol;
         int2 nx2 = nx;
         if ((j2 << CSH) >= ocnt) {
-            o2 = nx.y >> 8;
+            o2 = nx.y >> LB;
             ocnt2 = nx.x >> 21;
             ol2 = nx.x & OFF_MASK;
             j2 = 0;
-            nx2 = ws.ent[nx.y & 255];
+            nx2 = ws.ent[nx.y & IDM];
         }
         int idx2[CH];
         if (rd + 1 < R) {                               // (wave-uniform)
@@ -239,7 +247,7 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
         if (o != cur) {
             if (cur >= 0) atomicMin(&ws.key[cur], ((unsigned long long)bbits << 32) | (unsigned)(bpos << 12 | bidx));
             if (NP == M || cur < 0 || ((o ^ cur) & ROWS)) coop_fetch(ws, o & ROWS, st);
-            sc = ws.esc[o];
+            sc = ws.esc[srow(o)];
             cur = o;
             bbits = ~0u;
         }

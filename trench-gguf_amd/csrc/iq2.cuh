@@ -506,31 +506,33 @@ struct KIQ2XXS : Iq8Tab<256> {
 // (pieces of 2 measured 2% faster than 4, 11% faster than 8), IQ2_XS's two-shell lists more (4: 6% faster than 2)
 template <int GRID> constexpr int ch16() { return GRID == 1024 ? 2 : 4; }
 constexpr int IQ2XS_TW = 7;     // IQ2_XS's trial window (filtered search)
-// the search workspace of the 16-weight types: two trial scales of the lane's two groups as four lists (list
-// t*2 + k: trial t, group k), the two groups' values staged once (row k*64 + lane)
-using Iq16WS = CoopWSM<4, 16, true, 2>;
+// the search workspace of the 16-weight types: T trial scales of the lane's two groups as 2T lists (list t*2 + k:
+// trial t, group k), the two groups' values staged once (row k*64 + lane), one scale row a trial for T = 3
+template <int T> using Iq16WST = CoopWSM<2 * T, 16, true, 2, (T == 2 ? 4 : T)>;
+using Iq16WS = Iq16WST<2>;
 
-// the two groups' grid indices of every lane at two scales (all lanes call it together): list m = t*2 + k with
-// act[m] takes the grid point of group k's key at id[t] if the key is on the grid, else the winner of its neighbour
-// list (the distances at scale[t]), one wave-wide call for the four lists (the groups' values staged beforehand). A
-// search that accepts nothing flags the error (the reference traps) and yields index 0. Inactive lists get 0.
-template <int GRID>
-DEV void iq2_16_points(const bool (&act)[4], const float (&id)[2], const float (&scale)[2], const float (&xval)[16],
-                       const int32_t *map3, const QParams &p, const uint64_t *grid, Iq16WS &ws, int (&gi)[4],
-                       bool (&og)[4]) {
-    int mk[4], cnt[4], off[4], g[4];
-    float sc[4];
+// the two groups' grid indices of every lane at T scales (all lanes call it together): list m = t*2 + k with act[m]
+// takes the grid point of group k's key at id[t] if the key is on the grid, else the winner of its neighbour list
+// (the distances at scale[t]), one wave-wide call for the 2T lists (the groups' values staged beforehand). A search
+// that accepts nothing flags the error (the reference traps) and yields index 0. Inactive lists get 0.
+template <int GRID, int T = 2>
+DEV void iq2_16_points(const bool (&act)[2 * T], const float (&id)[T], const float (&scale)[T],
+                       const float (&xval)[16], const int32_t *map3, const QParams &p, const uint64_t *grid,
+                       Iq16WST<T> &ws, int (&gi)[2 * T], bool (&og)[2 * T]) {
+    constexpr int M = 2 * T;
+    int mk[M], cnt[M], off[M], g[M];
+    float sc[M];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
+    for (int m = 0; m < M; ++m) {
         mk[m] = act[m] ? map3[group_key3(xval + 8 * (m & 1), id[m >> 1])] : 0;
         og[m] = mk[m] >= 0;
         cnt[m] = act[m] && mk[m] < 0 ? m3_cnt(mk[m]) : 0;
         off[m] = act[m] && mk[m] < 0 ? m3_off(mk[m]) : 0;
         sc[m] = scale[m >> 1];
     }
-    coop_search_m<4, ch16<GRID>()>(cnt, off, sc, p.neigh, p.neigh_len, ws, EvalIq8{grid}, g);
+    coop_search_m<M, ch16<GRID>()>(cnt, off, sc, p.neigh, p.neigh_len, ws, EvalIq8{grid}, g);
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
+    for (int m = 0; m < M; ++m) {
         gi[m] = mk[m];
         if (act[m] && mk[m] < 0) {
             gi[m] = g[m];
@@ -542,9 +544,11 @@ DEV void iq2_16_points(const bool (&act)[4], const float (&id)[2], const float (
     }
 }
 
+// IQ2_S (GRID 1024) searches three trials a call (Iq16WST<3>), IQ2_XS two (Iq16WS)
+template <int GRID> using Iq16WSOf = Iq16WST<GRID == 1024 ? 3 : 2>;
 template <bool PARITY, int GRID>
 DEV float iq2_16_search(const float (&x)[16], const float (&qv)[16], float sigma2, float eps, const QParams &p,
-                        const uint8_t *lds, Iq16WS &ws, int (&gidx)[2], uint32_t (&bsg)[2], bool &live) {
+                        const uint8_t *lds, Iq16WSOf<GRID> &ws, int (&gidx)[2], uint32_t (&bsg)[2], bool &live) {
     const uint64_t *grid = Iq8Tab<GRID>::grid(lds);
     const int32_t *map3 = Iq8Tab<GRID>::map3(lds);
     float weight[16], waux[16], xval[16];
@@ -706,22 +710,26 @@ DEV float iq2_16_search(const float (&x)[16], const float (&qv)[16], float sigma
     // the two groups' values, staged once for all the trials and the final pass
 #pragma unroll
     for (int k = 0; k < 2; ++k) coop_stage<8>(ws, xval + 8 * k, waux + 8 * k, k * 64 + lane_id());
-    // the 19 trials two a call (the last call has one), accepted in trial order
+    // the 19 trials three a call (the last call has one: a wave-wide call costs much the same for few lists as for
+    // many), accepted in trial order
+    constexpr int TC = 3;
 #pragma unroll 1
-    for (int is = -9; is <= 9; is += 2) {
-        const bool two = is < 9;                    // (wave-uniform)
-        float id[2], tsc[2];
-        id[0] = (5 + is * 0.1f) / mx;
-        id[1] = (5 + (is + 1) * 0.1f) / mx;
-        tsc[0] = 1 / id[0];
-        tsc[1] = 1 / id[1];
-        const bool act[4] = {live, live, live && two, live && two};
-        int Pa[4];
-        bool og[4];
-        iq2_16_points<GRID>(act, id, tsc, xval, map3, p, grid, ws, Pa, og);
+    for (int is = -9; is <= 9; is += TC) {
+        const int nt = 10 - is < TC ? 10 - is : TC;     // trials is .. is + nt - 1 (wave-uniform)
+        float id[TC], tsc[TC];
+        bool act[2 * TC];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            if (t == 1 && !two) break;
+        for (int t = 0; t < TC; ++t) {
+            id[t] = (5 + (is + t) * 0.1f) / mx;
+            tsc[t] = 1 / id[t];
+            act[2 * t] = act[2 * t + 1] = live && t < nt;
+        }
+        int Pa[2 * TC];
+        bool og[2 * TC];
+        iq2_16_points<GRID, TC>(act, id, tsc, xval, map3, p, grid, ws, Pa, og);
+#pragma unroll
+        for (int t = 0; t < TC; ++t) {
+            if (t >= nt) break;
             float sumqx = 0, sumq2 = 0;
 #pragma unroll
             for (int k = 0; k < 2; ++k) sums_q8(weight + 8 * k, xval + 8 * k, grid[Pa[2 * t + k]], sumqx, sumq2);
@@ -738,11 +746,11 @@ DEV float iq2_16_search(const float (&x)[16], const float (&qv)[16], float sigma
     // (a group left at levels 0 is on the grid: on_grid stays true for it)
     const bool fin = live && (!on_grid[0] || !on_grid[1]) && scale > 0;
     {
-        const float id[2] = {1 / scale, 1 / scale}, fsc[2] = {scale, scale};
-        const bool act[4] = {fin && !on_grid[0], fin && !on_grid[1], false, false};
-        int gi[4];
-        bool og[4];
-        iq2_16_points<GRID>(act, id, fsc, xval, map3, p, grid, ws, gi, og);
+        const float id[TC] = {1 / scale, 1 / scale, 1 / scale}, fsc[TC] = {scale, scale, scale};
+        const bool act[2 * TC] = {fin && !on_grid[0], fin && !on_grid[1], false, false, false, false};
+        int gi[2 * TC];
+        bool og[2 * TC];
+        iq2_16_points<GRID, TC>(act, id, fsc, xval, map3, p, grid, ws, gi, og);
         float sumqx = 0, sumq2 = 0;
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
@@ -771,7 +779,7 @@ DEV float iq2_16_search(const float (&x)[16], const float (&qv)[16], float sigma
 
 // IQ2_S: block d qs[64] (32 grid bytes, 32 sign bytes) qh[8] scales[8] (82 bytes); lane g = 16-weight sub-block g
 struct KIQ2S : Iq8Tab<1024> {
-    static constexpr int BS = QK, G = 16, N = 16, BB = 82, WS = coop_wsm_bytes<4, 16, true, 2>(), WGW = 8;
+    static constexpr int BS = QK, G = 16, N = 16, BB = 82, WS = (int)sizeof(Iq16WSOf<1024>), WGW = 8;
     static constexpr bool QUEUE = true;         // (tiles of varying cost: the tile queue)
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
                           const QParams &p) {
@@ -784,7 +792,7 @@ struct KIQ2S : Iq8Tab<1024> {
         uint32_t bsg[2];
         bool live;
         const float scale = iq2_16_search<false, 1024>(x, qv, sigma2, EPS_IQ2S, p, lds,
-                                                       *(Iq16WS *)wave_ws<KIQ2S>(img), gidx, bsg, live);
+                                                       *(Iq16WSOf<1024> *)wave_ws<KIQ2S>(img), gidx, bsg, live);
         if (live) {
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
