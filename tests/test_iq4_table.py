@@ -1,0 +1,76 @@
+"""IQ4_NL / IQ4_XS codebook index (trench-gguf_amd/csrc/kquants.cuh, iq4_index): the kernel reads the interval
+kv[ml] <= x < kv[ml+1] from a table indexed by floor(x) clamped to [-128, 113] (NaN as 113), then applies the
+reference's nearer-end rule. Here that table and lookup, restated in numpy float32, against the reference's binary
+search best_index_int8 (gpuq/gpuq.hip:1286-1295) on a dense sample of all float32 bit patterns, every float within
+4096 ulps of each codebook value and each midpoint, and the special values."""
+import numpy as np
+
+KV = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], dtype=np.float32)
+
+
+def reference(x):
+    """best_index_int8: x <= kv[0] -> 0, x >= kv[15] -> 15, else bisection and the nearer end (ties up)"""
+    out = np.empty(x.shape, dtype=np.int64)
+    for i, v in enumerate(x):
+        if v <= KV[0]:
+            out[i] = 0
+            continue
+        if v >= KV[15]:
+            out[i] = 15
+            continue
+        lo, hi = 0, 15
+        while hi - lo > 1:
+            mid = (lo + hi) // 2
+            if v < KV[mid]:
+                hi = mid
+            else:
+                lo = mid
+        out[i] = hi - 1 if np.float32(v - KV[hi - 1]) < np.float32(KV[hi] - v) else hi
+    return out
+
+
+def table_index(x):
+    t = np.arange(-128, 114, dtype=np.float32)
+    ml_t = np.array([max([j for j in range(16) if KV[j] <= v] or [0]) for v in t])
+    f = np.minimum(np.maximum(np.floor(x), np.float32(-128)), np.float32(113))
+    fi = np.where(np.isnan(x), 241, np.nan_to_num(f, nan=113).astype(np.int64) + 128)
+    ml = ml_t[fi]
+    lo = KV[ml]
+    hi = KV[np.minimum(ml + 1, 15)]
+    with np.errstate(invalid="ignore"):
+        down = (ml == 15) | ((x - lo).astype(np.float32) < (hi - x).astype(np.float32))
+    return np.where(down, ml, ml + 1)
+
+
+def sample():
+    rng = np.random.default_rng(3)
+    bits = [np.arange(0, 1 << 32, 65521, dtype=np.uint64).astype(np.uint32),
+            rng.integers(0, 1 << 32, 200000, dtype=np.uint64).astype(np.uint32)]
+    marks = np.concatenate([KV, (KV[1:] + KV[:-1]) / 2, np.arange(-130, 117, dtype=np.float32)]).astype(np.float32)
+    for m in marks:
+        b = np.array([m], dtype=np.float32).view(np.uint32)[0]
+        d = np.arange(-4096, 4097, dtype=np.int64)
+        for sgn in (0, 0x80000000):
+            v = (np.int64(b) ^ sgn) + d
+            v = v[(v >= 0) & (v < (1 << 32))]
+            bits.append(v.astype(np.uint32))
+    x = np.concatenate(bits).view(np.float32)
+    special = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-45, -1e-45, 3.4e38, -3.4e38], dtype=np.float32)
+    return np.concatenate([x, special])
+
+
+def test_table_lookup_equals_reference_search():
+    x = sample()
+    got = table_index(x)
+    # the reference in numpy, vectorized: searchsorted for the bisection's bracket (kv[lo] <= x < kv[hi])
+    with np.errstate(invalid="ignore"):
+        hi = np.clip(np.searchsorted(KV, x, side="right"), 1, 15)
+        lo = hi - 1
+        near = np.where((x - KV[lo]).astype(np.float32) < (KV[hi] - x).astype(np.float32), lo, hi)
+        want = np.where(x <= KV[0], 0, np.where(x >= KV[15], 15, near))
+        want = np.where(np.isnan(x), 15, want)
+    assert np.array_equal(got, want), int((got != want).sum())
+    # the vectorized reference against the literal bisection on a slice (its NaN path included)
+    idx = np.random.default_rng(4).integers(0, x.size, 20000)
+    xs = np.concatenate([x[idx], np.array([np.nan, -np.inf, np.inf], dtype=np.float32)])
+    assert np.array_equal(reference(xs), table_index(xs))

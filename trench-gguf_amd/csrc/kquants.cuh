@@ -868,24 +868,43 @@ __constant__ float k_iq4f[16] = {-127.f, -104.f, -83.f, -65.f, -49.f, -35.f, -22
 
 // best_index_int8 over the IQ4 codebook (gpuq/gpuq.hip:1286-1295). For strictly increasing values the reference's
 // binary search always ends at the interval kv[ml] <= x < kv[ml+1] (ml = 15 for x >= kv[15] and for NaN, which its
-// false x < kv[mav] tests move up; ml = 0 for x < kv[1]), so four branch-free halving steps find the same ml; then
-// the nearer end with the reference's tie rule. (Checked equal to the reference's search on all 2^32 floats.)
-// Codebook values come from a 16-float LDS copy.
-DEV int iq4_index(float x, const float *kv, float &q) {
-    int ml = 0;
-    ml += !(x < kv[8]) ? 8 : 0;
-    ml += !(x < kv[ml + 4]) ? 4 : 0;
-    ml += !(x < kv[ml + 2]) ? 2 : 0;
-    ml += !(x < kv[ml + 1]) ? 1 : 0;
-    const int mu = ml < 15 ? ml + 1 : 15;
-    const float lo = kv[ml], hi = kv[mu];
-    const bool down = ml == 15 || x - lo < hi - x;
-    q = down ? lo : hi;
-    return down ? ml : mu;
+// false x < kv[mav] tests move up; ml = 0 for x < kv[1]); then the nearer end with the reference's tie rule. The
+// codebook values are integers, so kv[j] <= x exactly when kv[j] <= floor(x): the interval is a table entry indexed
+// by floor(x) clamped to [-128, 113] (NaN read as 113), one LDS read instead of the search's chain of dependent
+// reads (tests/test_iq4_table.py: equal to the reference's search on a dense sample of all floats, every float within
+// 4096 ulps of each codebook value and midpoint, and the special values).
+struct Iq4Ent {
+    float lo, hi;   // kv[ml], kv[min(ml + 1, 15)]
+    int ml, pad;
+};
+constexpr int IQ4_T0 = -128, IQ4_TN = 113 - IQ4_T0 + 1;    // table entries: floor(x) = -128 .. 113
+DEV int iq4_index(float x, const Iq4Ent *tab, float &q) {
+    const float f = fminf(fmaxf(floorf(x), (float)IQ4_T0), 113.f);
+    const int fi = x != x ? IQ4_TN - 1 : (int)f - IQ4_T0;
+    const Iq4Ent e = tab[fi];
+    const bool down = e.ml == 15 || x - e.lo < e.hi - x;
+    q = down ? e.lo : e.hi;
+    return down ? e.ml : e.ml + 1;
 }
+// the table (and the 16 codebook values before it), staged by a workgroup's threads
+DEV void iq4_stage(uint8_t *lds) {
+    float *kv = (float *)lds;
+    if (threadIdx.x < 16) kv[threadIdx.x] = k_iq4f[threadIdx.x];
+    Iq4Ent *tab = (Iq4Ent *)(lds + 64);
+    for (int i = threadIdx.x; i < IQ4_TN; i += blockDim.x) {
+        const float v = (float)(i + IQ4_T0);
+        int ml = 0;
+#pragma unroll
+        for (int j = 1; j < 16; ++j) ml = k_iq4f[j] <= v ? j : ml;
+        tab[i] = Iq4Ent{k_iq4f[ml], k_iq4f[ml < 15 ? ml + 1 : 15], ml, 0};
+    }
+}
+constexpr int IQ4_TAB = 64 + IQ4_TN * (int)sizeof(Iq4Ent);
+DEV const Iq4Ent *iq4_tab(const uint8_t *lds) { return (const Iq4Ent *)(lds + 64); }
 
 // one 32-weight sub-block's scale search; fills Lb, returns the scale (0 for a negligible block)
-DEV float iq4_block(const float (&xb)[32], const float (&weight)[32], Lv<32> &Lb, const float *kv) {
+DEV float iq4_block(const float (&xb)[32], const float (&weight)[32], Lv<32> &Lb, const float *kv,
+                    const Iq4Ent *tab) {
     float amax = 0, mx = 0;
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
@@ -900,7 +919,7 @@ DEV float iq4_block(const float (&xb)[32], const float (&weight)[32], Lv<32> &Lb
     for (int j = 0; j < 32; ++j) {
         const float al = id * xb[j];
         float q;
-        const int l = iq4_index(al, kv, q);
+        const int l = iq4_index(al, tab, q);
         Lb.put(j, (uint32_t)l);
         const float w = weight[j];
         sumqx += w * q * xb[j];
@@ -915,7 +934,7 @@ DEV float iq4_block(const float (&xb)[32], const float (&weight)[32], Lv<32> &Lb
         for (int j = 0; j < 32; ++j) {
             const float al = id * xb[j];
             float q;
-            (void)iq4_index(al, kv, q);
+            (void)iq4_index(al, tab, q);
             const float w = weight[j];
             sumqx += w * q * xb[j];
             sumq2 += w * q * q;
@@ -930,11 +949,9 @@ DEV float iq4_block(const float (&xb)[32], const float (&weight)[32], Lv<32> &Lb
 
 // IQ4_XS: block d scales_h scales_l[4] qs[128] (136 bytes); lane g = sub-block g
 struct KIQ4XS {
-    static constexpr int BS = QK, G = 8, N = 32, BB = 136, TAB = 64;
+    static constexpr int BS = QK, G = 8, N = 32, BB = 136, TAB = IQ4_TAB;
     static constexpr int WPE = 3;    // three waves a SIMD: 7% faster than two, for 140 bytes a lane of spill
-    static DEV void stage(const QParams &, uint8_t *lds) {
-        if (threadIdx.x < 16) ((float *)lds)[threadIdx.x] = k_iq4f[threadIdx.x];
-    }
+    static DEV void stage(const QParams &, uint8_t *lds) { iq4_stage(lds); }
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
                           const QParams &) {
         const float *kv = (const float *)lds;
@@ -954,7 +971,7 @@ struct KIQ4XS {
         }
         Lv<32> Lb;
         Lb.clear();
-        const float sd = iq4_block(x, weight, Lb, kv);
+        const float sd = iq4_block(x, weight, Lb, kv, iq4_tab(lds));
         const int jm = grp_argmax_first<G>(fabsf(sd), g);
         const float amax_scale = grp_bcast<G>(fabsf(sd), jm);
         const float max_scale = amax_scale > 0 ? grp_bcast<G>(sd, jm) : 0.f;   // (+0 when no |d| beat 0)
@@ -966,7 +983,7 @@ struct KIQ4XS {
         const float dl = d * l;
         const float idl = dl ? 1 / dl : 0.f;
 #pragma unroll
-        for (int j = 0; j < 32; ++j) { float q; Lb.put(j, (uint32_t)iq4_index(idl * x[j], kv, q)); }
+        for (int j = 0; j < 32; ++j) { float q; Lb.put(j, (uint32_t)iq4_index(idl * x[j], iq4_tab(lds), q)); }
         l += 32;
         if (g == 0) img_or16(img, boff, d16);
         img_or16(img, boff + 2, (uint32_t)((l >> 4) << (2 * g)));
@@ -980,10 +997,8 @@ struct KIQ4XS {
 
 // IQ4_NL: block d qs[16] (18 bytes), one lane a 32-block
 struct KIQ4NL {
-    static constexpr int BS = 32, G = 1, N = 32, BB = 18, TAB = 64;
-    static DEV void stage(const QParams &, uint8_t *lds) {
-        if (threadIdx.x < 16) ((float *)lds)[threadIdx.x] = k_iq4f[threadIdx.x];
-    }
+    static constexpr int BS = 32, G = 1, N = 32, BB = 18, TAB = IQ4_TAB;
+    static DEV void stage(const QParams &, uint8_t *lds) { iq4_stage(lds); }
     static DEV void quant(const float (&x)[N], const float *qwp, int, uint8_t *img, int boff, uint8_t *lds,
                           const QParams &) {
         const float *kv = (const float *)lds;
@@ -1003,11 +1018,11 @@ struct KIQ4NL {
         }
         Lv<32> Lb;
         Lb.clear();
-        const float s = iq4_block(x, weight, Lb, kv);
+        const float s = iq4_block(x, weight, Lb, kv, iq4_tab(lds));
         img_or16(img, boff, f2h(s));
         const float id = s ? 1 / s : 0;
 #pragma unroll
-        for (int j = 0; j < 32; ++j) { float q; Lb.put(j, (uint32_t)iq4_index(id * x[j], kv, q)); }
+        for (int j = 0; j < 32; ++j) { float q; Lb.put(j, (uint32_t)iq4_index(id * x[j], iq4_tab(lds), q)); }
         uint32_t wv[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) wv[k] = Lb.w[k] | (Lb.w[k + 4] << 4);
