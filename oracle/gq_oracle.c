@@ -1232,17 +1232,18 @@ static const int8_t k_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 
 
 /* index of the nearest codebook value, the lower one on ties away from it (gpuq/gpuq.hip:1286-1295) */
 static int nearest_iq4(float x) {
+    /* charged as the table form (the interval kv[ml] <= x < kv[ml+1] read from a table indexed by floor(x), the
+     * codebook values being integers): floor, clamp, NaN select, conversion, then the two differences, their
+     * compare and two selects; the bisection below gives the same index (tests/test_iq4_table.py) */
     const int8_t *val = k_iq4nl;
-    OPS(2);
+    OPS(9);
     if (x <= val[0]) return 0;
     if (x >= val[15]) return 15;
     int lo = 0, hi = 15;
     while (hi - lo > 1) {
         const int mid = (lo + hi) / 2;
         if (x < val[mid]) hi = mid; else lo = mid;
-        OPS(3);
     }
-    OPS(3);
     return x - val[hi - 1] < val[hi] - x ? hi - 1 : hi;
 }
 
