@@ -874,17 +874,19 @@ __constant__ float k_iq4f[16] = {-127.f, -104.f, -83.f, -65.f, -49.f, -35.f, -22
 // reads (tests/test_iq4_table.py: equal to the reference's search on a dense sample of all floats, every float within
 // 4096 ulps of each codebook value and midpoint, and the special values).
 struct Iq4Ent {
-    float lo, hi;   // kv[ml], kv[min(ml + 1, 15)]
-    int ml, pad;
+    float lo;       // kv[ml]
+    int mh;         // ml + 256 kv[min(ml + 1, 15)]: the upper end (an integer) is exactly (mh - ml) / 256
 };
 constexpr int IQ4_T0 = -128, IQ4_TN = 113 - IQ4_T0 + 1;    // table entries: floor(x) = -128 .. 113
 DEV int iq4_index(float x, const Iq4Ent *tab, float &q) {
     const float f = fminf(fmaxf(floorf(x), (float)IQ4_T0), 113.f);
     const int fi = x != x ? IQ4_TN - 1 : (int)f - IQ4_T0;
     const Iq4Ent e = tab[fi];
-    const bool down = e.ml == 15 || x - e.lo < e.hi - x;
-    q = down ? e.lo : e.hi;
-    return down ? e.ml : e.ml + 1;
+    const int ml = e.mh & 15;
+    const float hi = (float)((e.mh - ml) / 256);
+    const bool down = ml == 15 || x - e.lo < hi - x;
+    q = down ? e.lo : hi;
+    return down ? ml : ml + 1;
 }
 // the table (and the 16 codebook values before it), staged by a workgroup's threads
 DEV void iq4_stage(uint8_t *lds) {
@@ -896,7 +898,7 @@ DEV void iq4_stage(uint8_t *lds) {
         int ml = 0;
 #pragma unroll
         for (int j = 1; j < 16; ++j) ml = k_iq4f[j] <= v ? j : ml;
-        tab[i] = Iq4Ent{k_iq4f[ml], k_iq4f[ml < 15 ? ml + 1 : 15], ml, 0};
+        tab[i] = Iq4Ent{k_iq4f[ml], ml + 256 * (int)k_iq4f[ml < 15 ? ml + 1 : 15]};
     }
 }
 constexpr int IQ4_TAB = 64 + IQ4_TN * (int)sizeof(Iq4Ent);
