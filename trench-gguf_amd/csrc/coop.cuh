@@ -87,15 +87,32 @@ DEV int div_small(int a, int b) {
 }
 
 // The deal's mark table: walker L's first piece is L*R; this lane's lists hold pieces [s0, s0 + sum np) of the wave's
-// concatenation, list m the np[m] pieces after those of lists 0..m-1. For each walker whose first piece falls in them
-// (at most a few: the lane's pieces over R), mark[L] = (m*64 + lane) | (the piece's number in list m << SH).
-template <int M, int SH> DEV void deal_marks(int *mark, const int (&np)[M], int s0, int R) {
+// concatenation, list m the np[m] pieces after those of lists 0..m-1. For each walker whose first piece falls in
+// them (at most a few: the lane's pieces over R), mark[L] = (m*64 + lane) | (the piece's number in list m << SH).
+// INC: list by list, the walkers starting in it R pieces apart (a few instructions a walker, a loop a list: for many
+// lists a lane or many walkers a lane); else walker by walker, each finding its list among the M (fewer loops).
+template <int M, int SH, bool INC = M >= 6>
+DEV void deal_marks(int *mark, const int (&np)[M], int s0, int R) {
     const int lane = lane_id();
+    if (INC) {
+        int L = div_small(s0 + R - 1, R);               // the first walker starting among the lane's pieces
+        int j = (int)__umul24((unsigned)L, (unsigned)R) - s0;   // its first piece, counted from list m's first
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            while (j < np[m] && L < 64) {
+                mark[L] = (m * 64 + lane) | (j << SH);
+                ++L;
+                j += R;
+            }
+            j -= np[m];
+        }
+        return;
+    }
     int tot = 0;
 #pragma unroll
     for (int m = 0; m < M; ++m) tot += np[m];
     const int lf = div_small(s0 + R - 1, R);
-    const int ll = div_small(s0 + tot - 1, R);           // (no pieces: ll < lf)
+    const int ll = div_small(s0 + tot - 1, R);          // (no pieces: ll < lf)
     for (int L = lf; L <= ll && L < 64; ++L) {
         int j = (int)__umul24((unsigned)L, (unsigned)R) - s0;   // the walker's first piece among the lane's
         int m = M - 1;

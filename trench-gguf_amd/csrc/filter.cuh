@@ -128,7 +128,7 @@ DEV void coop_filter(const int (&cnt)[W], const int (&off)[W], const int (&ntr)[
         int np[W];
 #pragma unroll
         for (int m = 0; m < W; ++m) np[m] = (cnt[m] + CH - 1) >> CSH;
-        deal_marks<W, 9>(ws.mark, np, incl - tot, R);
+        deal_marks<W, 9, true>(ws.mark, np, incl - tot, R);
     }
     wave_sync();
     const int p0 = (int)__umul24((unsigned)lane, (unsigned)R);   // this walker's first piece
@@ -229,12 +229,14 @@ DEV void coop_filter(const int (&cnt)[W], const int (&off)[W], const int (&ntr)[
 #pragma unroll
         for (int r = 0; r < CH; ++r) {
             const uint32_t lo = (uint32_t)pt[r], hi = (uint32_t)(pt[r] >> 32);
-            float A = 0.f, B = 0.f;                     // (B: -2 sum (w x) q)
+            // (B: -2 sum (w x) q. The first terms are products: an fma with a zero addend rounds the same, up to the
+            // sign of a zero, which the key clears)
+            float A = 0.f, B = 0.f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const float q = small_int_f((float)(((i < 4 ? lo : hi) >> (8 * (i % 4))) & 0xffu));
-                A = fmaf(w[i], q * q, A);
-                B = fmaf(nwx[i], q, B);
+                A = i ? fmaf(w[i], q * q, A) : w[0] * (q * q);
+                B = i ? fmaf(nwx[i], q, B) : nwx[0] * q;
             }
 #pragma unroll
             for (int t = 0; t < W; ++t) {
