@@ -8,6 +8,10 @@
  * Conventions (as the reference's):
  *   - ggml type ids: Q8_0 8, Q2_K 10, Q3_K 11, Q4_K 12, Q5_K 13, Q6_K 14, IQ2_XXS 16, IQ2_XS 17, IQ3_XXS 18,
  *     IQ1_S 19, IQ4_NL 20, IQ3_S 21, IQ2_S 22, IQ4_XS 23, IQ1_M 29; sources F32 0, F16 1, Q8_0 8, BF16 30, MXFP4 39.
+ *   - Also quantized here (the reference leaves them to ggml on the CPU): llama-quantize's fallback types for rows
+ *     that are not whole 256-weight super-blocks, Q4_0 2, Q5_0 6, Q5_1 7 (32-weight blocks, with or without an
+ *     imatrix) and F16 1 (one value a block, rows of any length from F32 / F16 / BF16 sources; the imatrix ignored),
+ *     through gpuq_quantize*, gpuq_requantize* and gpuq_requantize_dev (tools/requant_experts.py:180-192).
  *   - Host entry points take host pointers, are synchronous and return the bytes written, 0 on any error.
  *   - Device entry points (*_dev) take device pointers, enqueue on `stream` (a hipStream_t, NULL = the null
  *     stream) without synchronizing, and return the bytes the launch will write, 0 on error.
@@ -35,7 +39,8 @@ extern "C" {
  * captured before it go on reading them); it must not overlap calls from other threads. */
 int gpuq_init(const char *tables_path, int device);
 
-/* gpuq/gpuq.hip:2082 gpuq_block_bytes: bytes of one block of the type, 0 for an unknown type */
+/* gpuq/gpuq.hip:2082 gpuq_block_bytes: bytes of one block of the type, 0 for an unknown type (F16: 2, a block
+ * being one value, as ggml's type size) */
 size_t gpuq_block_bytes(int type);
 
 /* gpuq/gpuq.hip:2213 gpuq_can_quantize: 1 when gpuq_quantize* takes the type with (1) or without (0) an imatrix */

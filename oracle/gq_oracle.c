@@ -1806,6 +1806,110 @@ static void o_q8_0(const float *x, uint8_t *y) {
     OPS(32 + 2 * C_DIV + 2 + 32 * 4);
 }
 
+/* ------------------------------------------------------------------ llama-quantize's fallback types
+ * Q4_0 / Q5_0 / Q5_1 and F16, for rows that are not whole 256-weight super-blocks (tools/requant_experts.py:180-192);
+ * the reference writes them through ggml on the CPU (tools/requant_experts.py:732-747, ggml_quantize_chunk). ggml is a
+ * third-party library absent from the reference (llama.cpp's ggml-quants.c, the revision its build.sh compiles):
+ * without an imatrix quantize_row_q4_0_ref / q5_0_ref / q5_1_ref, with one quantize_row_q4_0_impl / q5_0_impl /
+ * q5_1_impl (weights qw * sqrt(sigma2 + x^2), sigma2 the mean of x^2 over the whole row; make_qx_quants(32, nmax, x,
+ * L, 1, weight) = sym_levels above, make_qkx3_quants(32, 31, ..., -0.9, 0.05, 36, false) = affine_levels above); F16
+ * is ggml_fp32_to_fp16_row (GGML_FP32_TO_FP16 a value). */
+
+/* C's float -> int8_t / uint8_t conversion as x86 builds of ggml perform it: cvttss2si (INT_MIN for NaN or out of
+ * range), then the low byte */
+static inline int cvt_i32_x86(float v) { return (v >= -2147483648.f && v < 2147483648.f) ? (int)v : INT32_MIN; }
+static inline int cvt_i8_x86(float v) { return (int)(int8_t)(uint8_t)((uint32_t)cvt_i32_x86(v) & 0xffu); }
+static inline uint8_t cvt_u8_x86(float v) { return (uint8_t)((uint32_t)cvt_i32_x86(v) & 0xffu); }
+
+/* 5-bit levels into ggml's Q5 layout: qh bit j (j < 16: value j, else value j), qs[j] = low nibbles of j, j + 16 */
+static void q5_pack(const uint8_t *lv, uint8_t *qh4, uint8_t *qs) {
+    uint32_t qh = 0;
+    for (int j = 0; j < 16; ++j) {
+        qs[j] = (uint8_t)((lv[j] & 0x0F) | ((lv[j + 16] & 0x0F) << 4));
+        qh |= ((lv[j] & 0x10u) >> 4) << j;
+        qh |= ((lv[j + 16] & 0x10u) >> 4) << (j + 16);
+    }
+    memcpy(qh4, &qh, 4);
+}
+
+/* Q4_0 (nmax 8, 18-byte blocks d qs[16]) and Q5_0 (nmax 16, 22 bytes d qh[4] qs[16]); qw NULL: the _ref rule */
+static void o_q0(int nmax, const float *x, const float *qw, float sigma2, uint8_t *y) {
+    uint8_t lv[32];
+    float d;
+    if (!qw) {
+        float amax = 0.0f, mx = 0.0f;
+        for (int j = 0; j < 32; ++j) {
+            const float v = x[j];
+            if (amax < fabsf(v)) { amax = fabsf(v); mx = v; }
+        }
+        d = mx / -(float)nmax;
+        const float id = d ? 1.0f / d : 0.0f;
+        for (int j = 0; j < 32; ++j) {
+            const int l = cvt_i8_x86(x[j] * id + ((float)nmax + 0.5f));
+            lv[j] = (uint8_t)GMIN(2 * nmax - 1, l);
+        }
+        OPS(32 * 3 + 2 * C_DIV + 32 * 5);
+    } else {
+        float w[32];
+        int8_t L[32];
+        iq_weights(qw, x, sigma2, w, 32);
+        d = sym_levels(32, nmax, x, L, w);
+        for (int j = 0; j < 32; ++j) lv[j] = (uint8_t)L[j];
+    }
+    put16(y, f32_to_f16(d));
+    if (nmax == 8) {
+        for (int j = 0; j < 16; ++j) y[2 + j] = (uint8_t)(lv[j] | (lv[j + 16] << 4));
+    } else {
+        q5_pack(lv, y + 2, y + 6);
+    }
+}
+
+/* Q5_1: d m qh[4] qs[16], x ~ d * l + m; qw NULL: the _ref rule */
+static void o_q5_1(const float *x, const float *qw, float sigma2, uint8_t *y) {
+    uint8_t lv[32];
+    float d, m;
+    if (!qw) {
+        float mn = FLT_MAX, mx = -FLT_MAX;
+        for (int j = 0; j < 32; ++j) {
+            if (x[j] < mn) mn = x[j];
+            if (x[j] > mx) mx = x[j];
+        }
+        d = (mx - mn) / ((1 << 5) - 1);
+        m = mn;
+        const float id = d ? 1.0f / d : 0.0f;
+        for (int j = 0; j < 32; ++j) lv[j] = cvt_u8_x86((x[j] - mn) * id + 0.5f);
+        OPS(32 * 2 + 2 * C_DIV + 32 * 4);
+    } else {
+        float w[32], the_min;
+        uint8_t Laux[32];
+        iq_weights(qw, x, sigma2, w, 32);
+        d = affine_levels(1, 32, 31, x, w, lv, &the_min, Laux, -0.9f, 0.05f, 36, 0);
+        m = -the_min;
+    }
+    put16(y, f32_to_f16(d));
+    put16(y + 2, f32_to_f16(m));
+    q5_pack(lv, y + 4, y + 8);
+}
+
+static int legacy_type(int type) { return type == GQO_Q4_0 || type == GQO_Q5_0 || type == GQO_Q5_1; }
+
+/* one row of a fallback type: the imatrix rules' sigma2 is sum(x^2) over the row, in index order, over its length */
+static void quant_row_legacy(int type, const float *x, int64_t n, const float *qw, uint8_t *y) {
+    float sigma2 = 0.f;
+    if (qw) {
+        float s = 0;
+        for (int64_t j = 0; j < n; ++j) s += x[j] * x[j];
+        sigma2 = s / (float)n;
+        OPS(2 * n + C_DIV);
+    }
+    const size_t bb = type == GQO_Q4_0 ? 18 : type == GQO_Q5_0 ? 22 : 24;
+    for (int64_t ib = 0; ib < n / 32; ++ib) {
+        const float *xb = x + 32 * ib, *wb = qw ? qw + 32 * ib : NULL;
+        if (type == GQO_Q5_1) o_q5_1(xb, wb, sigma2, y + ib * bb);
+        else o_q0(type == GQO_Q4_0 ? 8 : 16, xb, wb, sigma2, y + ib * bb);
+    }
+}
+
 /* ------------------------------------------------------------------ type traits and dispatch */
 size_t gqo_block_bytes(int type) {
     switch (type) {
@@ -1824,10 +1928,18 @@ size_t gqo_block_bytes(int type) {
         case GQO_Q5_K: return 176;
         case GQO_Q6_K: return 210;
         case GQO_Q8_0: return 34;
+        case GQO_Q4_0: return 18;
+        case GQO_Q5_0: return 22;
+        case GQO_Q5_1: return 24;
+        case GQO_F16: return 2;
         default: return 0;
     }
 }
-int gqo_block_len(int type) { return type == GQO_IQ4_NL || type == GQO_Q8_0 ? 32 : (gqo_block_bytes(type) ? QK : 0); }
+int gqo_block_len(int type) {
+    if (type == GQO_F16) return 1;
+    if (type == GQO_IQ4_NL || type == GQO_Q8_0 || legacy_type(type)) return 32;
+    return gqo_block_bytes(type) ? QK : 0;
+}
 
 static int needs_tables(int type) {
     return type == GQO_IQ2_XXS || type == GQO_IQ2_XS || type == GQO_IQ2_S || type == GQO_IQ1_S || type == GQO_IQ1_M ||
@@ -1835,7 +1947,7 @@ static int needs_tables(int type) {
 }
 static int takes_no_imatrix(int type) {
     return type == GQO_Q2_K || type == GQO_Q3_K || type == GQO_Q4_K || type == GQO_Q5_K || type == GQO_Q6_K ||
-           type == GQO_Q8_0 || type == GQO_IQ4_NL || type == GQO_IQ4_XS;
+           type == GQO_Q8_0 || type == GQO_IQ4_NL || type == GQO_IQ4_XS || legacy_type(type) || type == GQO_F16;
 }
 
 static void quant_block(int type, const float *x, const float *qw, uint8_t *y, const otab *t) {
@@ -1870,11 +1982,23 @@ size_t gqo_quantize_chunk(int type, const float *src, void *dst, int64_t start, 
         t = tab_search(type);
         if (!t) return 0;
     }
-    if (type == GQO_Q8_0) imatrix = NULL;   /* (ggml_quantize_chunk ignores it for Q8_0) */
+    if (type == GQO_Q8_0 || type == GQO_F16) imatrix = NULL;   /* (ggml_quantize_chunk ignores it for these) */
     const int64_t nb_row = n_per_row / bs;
     const size_t row_size = (size_t)nb_row * bb;
     uint8_t *out = (uint8_t *)dst + (size_t)(start / n_per_row) * row_size;
     t_err = 0;
+    if (type == GQO_F16) {
+        for (int64_t i = 0; i < nrows * n_per_row; ++i) put16(out + 2 * i, f32_to_f16(src[start + i]));
+        ops_flush();
+        return (size_t)nrows * row_size;
+    }
+    if (legacy_type(type)) {
+        for (int64_t r = 0; r < nrows; ++r)
+            quant_row_legacy(type, src + start + r * n_per_row, n_per_row, imatrix, out + r * row_size);
+        ops_flush();
+        stat_flush();
+        return (size_t)nrows * row_size;
+    }
     for (int64_t r = 0; r < nrows; ++r) {
         const float *x = src + start + r * n_per_row;
         for (int64_t ib = 0; ib < nb_row; ++ib)

@@ -19,7 +19,7 @@ extern "C" {
 
 /* ggml type ids (gpuq/gpuq.hip:54-55, 2106) */
 enum {
-    GQO_F32 = 0, GQO_F16 = 1, GQO_Q8_0 = 8, GQO_Q2_K = 10, GQO_Q3_K = 11, GQO_Q4_K = 12, GQO_Q5_K = 13,
+    GQO_F32 = 0, GQO_F16 = 1, GQO_Q4_0 = 2, GQO_Q5_0 = 6, GQO_Q5_1 = 7, GQO_Q8_0 = 8, GQO_Q2_K = 10, GQO_Q3_K = 11, GQO_Q4_K = 12, GQO_Q5_K = 13,
     GQO_Q6_K = 14, GQO_IQ2_XXS = 16, GQO_IQ2_XS = 17, GQO_IQ3_XXS = 18, GQO_IQ1_S = 19, GQO_IQ4_NL = 20,
     GQO_IQ3_S = 21, GQO_IQ2_S = 22, GQO_IQ4_XS = 23, GQO_IQ1_M = 29, GQO_BF16 = 30, GQO_MXFP4 = 39
 };

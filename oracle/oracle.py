@@ -14,9 +14,11 @@ QUANT_TYPES = [Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ2_XXS, IQ2_XS, IQ3_XXS, IQ1
                IQ1_M]
 TABLE_TYPES = [IQ2_XXS, IQ2_XS, IQ3_XXS, IQ1_S, IQ3_S, IQ2_S, IQ1_M]
 NO_IMATRIX_OK = [Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS]
+Q4_0, Q5_0, Q5_1 = 2, 6, 7
+FALLBACK_TYPES = [Q4_0, Q5_0, Q5_1, F16]     # llama-quantize's types for rows that are not whole super-blocks
 NAMES = {Q8_0: "q8_0", Q2_K: "q2_k", Q3_K: "q3_k", Q4_K: "q4_k", Q5_K: "q5_k", Q6_K: "q6_k", IQ2_XXS: "iq2_xxs",
          IQ2_XS: "iq2_xs", IQ3_XXS: "iq3_xxs", IQ1_S: "iq1_s", IQ4_NL: "iq4_nl", IQ3_S: "iq3_s", IQ2_S: "iq2_s",
-         IQ4_XS: "iq4_xs", IQ1_M: "iq1_m"}
+         IQ4_XS: "iq4_xs", IQ1_M: "iq1_m", Q4_0: "q4_0", Q5_0: "q5_0", Q5_1: "q5_1", F16: "f16"}
 
 _vp, _i64, _sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_size_t
 

@@ -41,7 +41,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 def test_block_bytes(lib):
     want = {8: 34, 10: 84, 11: 110, 12: 144, 13: 176, 14: 210, 16: 66, 17: 74, 18: 98, 19: 50, 20: 18, 21: 110,
-            22: 82, 23: 136, 29: 56, 0: 0, 1: 0, 30: 0, 39: 0, 7: 0}
+            22: 82, 23: 136, 29: 56, 2: 18, 6: 22, 7: 24, 1: 2, 0: 0, 30: 0, 39: 0, 3: 0, 9: 0}
     for t, b in want.items():
         assert lib.gpuq_block_bytes(t) == b, t
 

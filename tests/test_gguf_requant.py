@@ -183,8 +183,10 @@ def test_plan_and_check_mode(tmp_path, capsys):
     assert "no imatrix" in plan["blk.0.ffn_down_exps.weight"].note
     assert plan["blk.0.attn_norm.weight"].new_type is None and "not a matrix" in plan["blk.0.attn_norm.weight"].note
     assert plan["blk.0.attn_q.weight"].new_type is None                   # already Q8_0
-    with pytest.raises(requant.RequantError, match="does not quantize Q5_0"):   # 96-long rows: Q4_K -> Q5_0
-        requant.plan_shard(r, rules[3:], {})
+    s = requant.plan_shard(r, rules[3:], {})[-1]                          # 96-long rows: Q4_K -> Q5_0
+    assert s.new_type == T["Q5_0"] and "fallback" in s.note and s.nbytes == 5 * 3 * 22
+    with pytest.raises(requant.RequantError, match="does not quantize Q5_0"):   # (a library without it)
+        requant.plan_shard(r, rules[3:], {}, can_quantize=lambda typ, with_im: typ != T["Q5_0"])
     im = {"blk.0.ffn_down_exps.weight": np.ones((4, 512), np.float32)}
     s = requant.plan_shard(r, rules[:1], im)[0]
     assert s.new_type == T["IQ2_XXS"] and s.nbytes == 4 * 64 * 2 * 66 and s.imatrix is im[s.tensor.name]
@@ -253,7 +255,9 @@ def gq():
 @pytest.mark.gpu
 def test_requant_gguf_matches_oracle(tmp_path, gq):
     """a two-shard model: BF16 experts -> IQ2_XXS, MXFP4 experts -> IQ1_M, F32 -> Q8_0 and F16 -> Q4_K without an
-    imatrix, 640-long rows -> IQ4_NL (the fallback), the rest copied; the second shard also with --only-matched"""
+    imatrix, 640-long rows -> IQ4_NL (the fallback), llama-quantize's other fallbacks (96-long rows asked Q4_K -> Q5_0
+    with an imatrix, 160-long F16 rows asked Q5_K -> Q5_1, 100-long BF16 rows asked Q2_K -> F16), the rest copied; the
+    second shard also with --only-matched"""
     from oracle import Oracle
     orc = Oracle(tables=gpuq.tables_path())
     rng = np.random.default_rng(11)
@@ -266,15 +270,21 @@ def test_requant_gguf_matches_oracle(tmp_path, gq):
     f32 = (rng.standard_normal((8, ne0)) * 0.02).astype(np.float32)
     f16 = (rng.standard_normal((4, ne0)) * 0.02).astype(np.float16)
     nl = (rng.standard_normal((6, 640)) * 0.02).astype(np.float32)
+    q50 = (rng.standard_normal((5, 96)) * 0.02).astype(np.float32)
+    q51 = (rng.standard_normal((4, 160)) * 0.02).astype(np.float16)
+    b100 = (rng.standard_normal((3, 100)).astype(np.float32) * 0.02).view(np.uint32)
+    b100 = ((b100 + 0x7FFF + ((b100 >> 16) & 1)) >> 16).astype(np.uint16)
     norm = rng.standard_normal(ne0).astype(np.float32)
     ims = {n: rng.lognormal(0, 1.5, shp).astype(np.float32) for n, shp in (
         ("blk.0.ffn_up_exps.weight", (nexp, ne0)), ("blk.0.ffn_down_exps.weight", (nexp, ne0)),
-        ("blk.1.fallback.weight", (1, 640)))}
+        ("blk.1.fallback.weight", (1, 640)), ("blk.1.q50.weight", (1, 96)))}
     shard = [
         [("blk.0.ffn_up_exps.weight", T["BF16"], (ne0, ne1, nexp), bf16), ("blk.0.norm.weight", T["F32"], (ne0,), norm),
          ("blk.0.ffn_down_exps.weight", T["MXFP4"], (ne0, ne1, nexp), mx)],
         [("blk.1.attn_q.weight", T["F32"], (ne0, 8), f32), ("blk.1.attn_k.weight", T["F16"], (ne0, 4), f16),
-         ("blk.1.fallback.weight", T["F32"], (640, 6), nl), ("blk.1.keep.weight", T["F32"], (ne0, 8), f32)],
+         ("blk.1.fallback.weight", T["F32"], (640, 6), nl), ("blk.1.keep.weight", T["F32"], (ne0, 8), f32),
+         ("blk.1.q50.weight", T["F32"], (96, 5), q50), ("blk.1.q51.weight", T["F16"], (160, 4), q51),
+         ("blk.1.f16.weight", T["BF16"], (100, 3), b100)],
     ]
     src = tmp_path / "src"
     src.mkdir()
@@ -298,12 +308,14 @@ def test_requant_gguf_matches_oracle(tmp_path, gq):
             w.write_tensor_data(a)
             w.write_tensor_data(np.ones(a.shape[0], np.float32))
     rules = tmp_path / "rules.txt"
-    rules.write_text("ffn_up_exps iq2_xxs\nffn_down_exps iq1_m\nattn_q q8_0\nattn_k q4_k\nfallback iq2_xxs\n")
+    rules.write_text("ffn_up_exps iq2_xxs\nffn_down_exps iq1_m\nattn_q q8_0\nattn_k q4_k\nfallback iq2_xxs\n"
+                     "q50 q4_k\nq51 q5_k\nf16 q2_k\n")
     out = tmp_path / "out"
     requant.run(str(src / "m-00001-of-00002.gguf"), str(out), str(rules), imp, gq=gq)
     want_types = {"blk.0.ffn_up_exps.weight": T["IQ2_XXS"], "blk.0.ffn_down_exps.weight": T["IQ1_M"],
                   "blk.1.attn_q.weight": T["Q8_0"], "blk.1.attn_k.weight": T["Q4_K"],
-                  "blk.1.fallback.weight": T["IQ4_NL"]}
+                  "blk.1.fallback.weight": T["IQ4_NL"], "blk.1.q50.weight": T["Q5_0"], "blk.1.q51.weight": T["Q5_1"],
+                  "blk.1.f16.weight": T["F16"]}
     for i, tensors in enumerate(shard):
         name = "m-%05d-of-00002.gguf" % (i + 1)
         r, s = gguf_io.GGUFReader(str(out / name)), gguf_io.GGUFReader(str(src / name))
@@ -318,7 +330,11 @@ def test_requant_gguf_matches_oracle(tmp_path, gq):
             assert t.tensor_type == typ, t.name
             n0 = st.shape[0]
             nmat = st.shape[2] if len(st.shape) == 3 else 1
-            x = orc.decode_src(st.tensor_type, np.ascontiguousarray(st.data), st.n_elements).reshape(nmat, -1, n0)
+            if st.tensor_type == T["BF16"] and n0 % 32:          # (the oracle's decoder takes 32-value blocks)
+                x = (np.ascontiguousarray(st.data).view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+                x = x.reshape(nmat, -1, n0)
+            else:
+                x = orc.decode_src(st.tensor_type, np.ascontiguousarray(st.data), st.n_elements).reshape(nmat, -1, n0)
             im = ims.get(t.name) if typ != T["Q4_K"] else None
             rows = [orc.quantize(typ, x[e], None if im is None or typ == T["Q8_0"] else im[e]) for e in range(nmat)]
             assert np.array_equal(t.data, np.concatenate([a.reshape(-1) for a in rows])), t.name
@@ -327,7 +343,8 @@ def test_requant_gguf_matches_oracle(tmp_path, gq):
     requant.run(str(src / "m-00001-of-00002.gguf"), str(out2), str(rules), imp, gq=gq, only_matched=True)
     r = gguf_io.GGUFReader(str(out2 / "m-00002-of-00002.gguf"))
     assert list(r.fields) == ["general.architecture"]
-    assert [t.name for t in r.tensors] == ["blk.1.attn_q.weight", "blk.1.attn_k.weight", "blk.1.fallback.weight"]
+    assert [t.name for t in r.tensors] == ["blk.1.attn_q.weight", "blk.1.attn_k.weight", "blk.1.fallback.weight",
+                                           "blk.1.q50.weight", "blk.1.q51.weight", "blk.1.f16.weight"]
     full = gguf_io.GGUFReader(str(out / "m-00002-of-00002.gguf"))
     for t in r.tensors:
         assert np.array_equal(t.data, full.tensor(t.name).data)

@@ -40,6 +40,9 @@ struct QParams {
     // b*sb_stride + sb_off, its importance at row*qw_stride + qw_off, and writes its block at byte
     // b*out_stride + out_off. The contiguous defaults are sb_stride = BS, qw_stride = BS, out_stride = BB, 0 offsets.
     int64_t sb_stride, sb_off, qw_stride, qw_off, out_stride, out_off;
+    // the row-wide sigma2 of the Q4_0 / Q5_0 / Q5_1 imatrix rules (one a row: unit b is in row b / row_units)
+    const float *rsig;
+    int64_t row_units;
 };
 
 // map3 entries: >= 0 a grid index; < 0 an off-grid key, -1 - (list offset | list length << M3_OFF_BITS)
@@ -140,6 +143,9 @@ template <class T> struct wgw_of<T, decltype((void)T::WGW)> { static constexpr i
 // resident grid; without it a grid-stride order over up to 32 waves a CU (tiles of equal cost)
 template <class T, class = void> struct queue_of { static constexpr bool v = false; };
 template <class T> struct queue_of<T, decltype((void)T::QUEUE)> { static constexpr bool v = T::QUEUE; };
+// ROWSIG (optional): quant_rs takes the unit's row-wide sigma2 (p.rsig) after its importance row
+template <class T, class = void> struct rowsig_of { static constexpr bool v = false; };
+template <class T> struct rowsig_of<T, decltype((void)T::ROWSIG)> { static constexpr bool v = T::ROWSIG; };
 // WPE (optional): the waves per SIMD the register allocation must allow (default 2)
 template <class T, class = void> struct wpe_of { static constexpr int v = 2; };
 template <class T> struct wpe_of<T, decltype((void)T::WPE)> { static constexpr int v = T::WPE; };
@@ -177,7 +183,10 @@ __global__ __launch_bounds__(64 * wgw_of<T>::v) __attribute__((amdgpu_waves_per_
         // the next chunk, asked for at a chunk's first tile (lane 0's atomic returns while the chunk is quantized)
         if (queue && k == 0 && lane == 0) tn = atomicAdd(p.tiles, 1ull);
         const float *qw = p.qw ? p.qw + qw_row(p, b) * p.qw_stride + p.qw_off + g * T::N : nullptr;
-        T::quant(x, qw, g, img, slot * T::BB, lds, p);
+        if constexpr (rowsig_of<T>::v)
+            T::quant_rs(x, qw, qw ? p.rsig[b / p.row_units] : 0.f, g, img, slot * T::BB, lds, p);
+        else
+            T::quant(x, qw, g, img, slot * T::BB, lds, p);
         wave_sync();
         if (p.out_stride == T::BB && p.out_off == 0) {
             img_store(p.dst + b0 * T::BB, img, nact * T::BB);

@@ -22,6 +22,7 @@
 #include "common.cuh"
 #include "frame.cuh"
 #include "kquants.cuh"
+#include "legacy.cuh"
 #include "iq2.cuh"
 #include "iq1.cuh"
 #include "iq3.cuh"
@@ -271,6 +272,9 @@ template <int SRC> bool dispatch_src(int type, const QParams &p, hipStream_t st)
             return launch_q<KQ80, SRC>(p, st);
         case T_IQ4_NL: return launch_q<KIQ4NL, SRC>(p, st);
         case T_IQ4_XS: return launch_q<KIQ4XS, SRC>(p, st);
+        case T_Q4_0: return launch_q<KQ40, SRC>(p, st);
+        case T_Q5_0: return launch_q<KQ50, SRC>(p, st);
+        case T_Q5_1: return launch_q<KQ51, SRC>(p, st);
         case T_IQ2_XXS: return launch_q<KIQ2XXS, SRC>(p, st);
         case T_IQ2_XS: return launch_q<KIQ2XS, SRC>(p, st);
         case T_IQ2_S: return launch_q<KIQ2S, SRC>(p, st);
@@ -327,9 +331,16 @@ bool launch_decode(int src, const void *in, float *out, int64_t n, hipStream_t s
 
 bool takes_no_imatrix(int t) {
     return t == T_Q2_K || t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_Q8_0 || t == T_IQ4_NL ||
-           t == T_IQ4_XS;
+           t == T_IQ4_XS || t == T_Q4_0 || t == T_Q5_0 || t == T_Q5_1 || t == T_F16;
 }
-int block_len(int t) { return t == T_IQ4_NL || t == T_Q8_0 ? 32 : QK; }
+// ggml's block length of an output type (F16: one value)
+int block_len(int t) {
+    return t == T_F16 ? 1 : t == T_IQ4_NL || t == T_Q8_0 || t == T_Q4_0 || t == T_Q5_0 || t == T_Q5_1 ? 32 : QK;
+}
+// the 32-weight types whose imatrix rule weighs by the row-wide sigma2
+bool rowsig_type(int t) { return t == T_Q4_0 || t == T_Q5_0 || t == T_Q5_1; }
+// sources F16 output reads value by value, for rows of any length
+bool elementwise_src(int src) { return src == T_F32 || src == T_F16 || src == T_BF16; }
 bool needs_tables(int t) { return is_search_type(t) || t == T_IQ1_M; }
 
 int64_t src_bytes(int src, int64_t n) {
@@ -348,7 +359,7 @@ QParams params_for(int type, const void *src, void *dst, int64_t nunits, const f
     p.src = (const uint8_t *)src;
     p.dst = (uint8_t *)dst;
     p.nsb = nunits;
-    p.qw = type == T_Q8_0 ? nullptr : qw;   // (ggml_quantize_chunk ignores the imatrix for Q8_0)
+    p.qw = type == T_Q8_0 || type == T_F16 ? nullptr : qw;   // (ggml_quantize_chunk ignores the imatrix for these)
     p.qw_mat = qw_mat;
     p.qw_mod = qw_mod;
     p.qw_div = qw_div;
@@ -375,6 +386,43 @@ bool type_ok(int type, int64_t n_per_row, bool with_imatrix) {
     if (needs_tables(type) && !tab_of(type).ok) return false;
     if (!with_imatrix && !takes_no_imatrix(type)) return false;
     return n_per_row > 0 && n_per_row % block_len(type) == 0;
+}
+
+// One launch of `rows` rows of n_per_row values (p: the quantize parameters of those rows' units): F16 one value a
+// thread; the Q4_0 / Q5_0 / Q5_1 imatrix rules first write every row's sigma2 into sig (rows floats); the rest the
+// quantize kernel.
+bool launch_rows(int type, int src, QParams p, int64_t rows, int64_t n_per_row, float *sig, hipStream_t st) {
+    if (type == T_F16) {
+        const int64_t n = rows * n_per_row;
+        const unsigned grid = (unsigned)((n + 255) / 256);
+        uint16_t *o = (uint16_t *)p.dst;
+        switch (src) {
+            case T_F32: hipLaunchKernelGGL((k_to_f16<T_F32>), dim3(grid), dim3(256), 0, st, p.src, o, n); break;
+            case T_F16: hipLaunchKernelGGL((k_to_f16<T_F16>), dim3(grid), dim3(256), 0, st, p.src, o, n); break;
+            case T_BF16: hipLaunchKernelGGL((k_to_f16<T_BF16>), dim3(grid), dim3(256), 0, st, p.src, o, n); break;
+            case T_Q8_0: hipLaunchKernelGGL((k_to_f16<T_Q8_0>), dim3(grid), dim3(256), 0, st, p.src, o, n); break;
+            case T_MXFP4: hipLaunchKernelGGL((k_to_f16<T_MXFP4>), dim3(grid), dim3(256), 0, st, p.src, o, n); break;
+            default: return false;
+        }
+        return hipGetLastError() == hipSuccess;
+    }
+    if (rowsig_type(type) && p.qw) {
+        const unsigned grid = (unsigned)((rows + 255) / 256);
+#define KSIG(S) hipLaunchKernelGGL((k_rowsig<S>), dim3(grid), dim3(256), 0, st, p.src, sig, rows, n_per_row)
+        switch (src) {
+            case T_F32: KSIG(T_F32); break;
+            case T_F16: KSIG(T_F16); break;
+            case T_BF16: KSIG(T_BF16); break;
+            case T_Q8_0: KSIG(T_Q8_0); break;
+            case T_MXFP4: KSIG(T_MXFP4); break;
+            default: return false;
+        }
+#undef KSIG
+        if (hipGetLastError() != hipSuccess) return false;
+        p.rsig = sig;
+        p.row_units = n_per_row / 32;
+    }
+    return dispatch(type, src, p, st);
 }
 
 // ------------------------------------------------------------------ the host API's streamed pipeline
@@ -408,6 +456,7 @@ struct PinBuf {
 constexpr int NSLOT = 3;
 struct Slot {
     Buf in, out;                      // device: source bytes, blocks
+    Buf sig;                          // device: the rows' sigma2 (Q4_0 / Q5_0 / Q5_1 with an imatrix)
     PinBuf pin_in, pin_out;
     hipEvent_t copied = nullptr;      // the slot's H2D copy is done: pin_in may be refilled
     hipEvent_t quantized = nullptr;   // the slot's kernels are done: in and f32 may be refilled, out is complete
@@ -468,7 +517,7 @@ size_t quantize_host(int src, const void *raw, int type, void *dst, int64_t nmat
                      const float *imatrix) {
     if (nmat <= 0 || nrow <= 0 || !type_ok(type, n_per_row, imatrix != nullptr)) return 0;
     const int64_t row_src = src_bytes(src, n_per_row);
-    if (!row_src || n_per_row % 32) return 0;
+    if (!row_src || (n_per_row % 32 && !(type == T_F16 && elementwise_src(src)))) return 0;
     std::lock_guard<std::mutex> lock(g_mu);
     if (!pipe_ready()) return 0;
     const int64_t nb_row = n_per_row / block_len(type), nb_mat = nrow * nb_row, rows = nmat * nrow;
@@ -487,12 +536,13 @@ size_t quantize_host(int src, const void *raw, int type, void *dst, int64_t nmat
     const int64_t max_rows = std::min(rows, std::max<int64_t>(1, budget / row_src));
     for (Slot &s : g_slot) {
         if (!s.in.grow((size_t)(max_rows * row_src) + 16) || !s.out.grow((size_t)(max_rows * row_out) + 16) ||
-            !s.pin_in.grow((size_t)(max_rows * row_src)) || !s.pin_out.grow((size_t)(max_rows * row_out)))
+            !s.pin_in.grow((size_t)(max_rows * row_src)) || !s.pin_out.grow((size_t)(max_rows * row_out)) ||
+            (rowsig_type(type) && imatrix && !s.sig.grow((size_t)max_rows * 4)))
             return 0;
         s.used = false;
     }
     const float *qw = nullptr;
-    if (imatrix && type != T_Q8_0) {
+    if (imatrix && type != T_Q8_0 && type != T_F16) {
         if (!g_qw.grow((size_t)nmat * n_per_row * 4)) return 0;
         if (hipMemcpy(g_qw.p, imatrix, (size_t)nmat * n_per_row * 4, hipMemcpyHostToDevice) != hipSuccess) return 0;
         qw = (const float *)g_qw.p;
@@ -525,7 +575,8 @@ size_t quantize_host(int src, const void *raw, int type, void *dst, int64_t nmat
         if (ok) {
             const float *cqw = qw ? qw + (r0 / nrow) * n_per_row : nullptr;
             const QParams p = params_for(type, s.in.p, s.out.p, cr * nb_row, cqw, nb_mat, nb_row, 1);
-            ok = dispatch(type, src, p, g_st_q) && hipEventRecord(s.quantized, g_st_q) == hipSuccess;
+            ok = launch_rows(type, src, p, cr, n_per_row, (float *)s.sig.p, g_st_q) &&
+                 hipEventRecord(s.quantized, g_st_q) == hipSuccess;
         }
         // blocks -> pinned (the slot's previous blocks were taken out of pin_out by the last iteration)
         ok = ok && hipStreamWaitEvent(g_st_out, s.quantized, 0) == hipSuccess &&
@@ -707,6 +758,10 @@ extern "C" size_t gpuq_block_bytes(int type) {
         case T_Q5_K: return 176;
         case T_Q6_K: return 210;
         case T_Q8_0: return 34;
+        case T_Q4_0: return 18;
+        case T_Q5_0: return 22;
+        case T_Q5_1: return 24;
+        case T_F16: return 2;
         default: return 0;
     }
 }
@@ -799,12 +854,33 @@ extern "C" size_t gpuq_dequantize_src_dev(int src, const void *d_raw, float *d_o
 extern "C" size_t gpuq_requantize_dev(int src, const void *d_raw, int type, void *d_dst, int64_t nmat, int64_t nrow,
                                       int64_t n_per_row, const float *d_imatrix, void *stream) {
     if (nmat <= 0 || nrow <= 0 || !fused_src(src) || !type_ok(type, n_per_row, d_imatrix != nullptr)) return 0;
-    if (n_per_row % 32 || !src_aligned(src, d_raw, n_per_row)) return 0;
+    if (type == T_F16) {    // value by value: any row length from F32 / F16 / BF16, element-aligned
+        const uintptr_t am = src == T_F32 ? 3 : src == T_MXFP4 ? 0 : 1;
+        if ((n_per_row % 32 && !elementwise_src(src)) || ((uintptr_t)d_raw & am)) return 0;
+    } else if (n_per_row % 32 || !src_aligned(src, d_raw, n_per_row)) {
+        return 0;
+    }
     if ((d_imatrix && ((uintptr_t)d_imatrix & 15)) || ((uintptr_t)d_dst & 1)) return 0;
+    const hipStream_t st = (hipStream_t)stream;
     const int bs = block_len(type);
-    const int64_t nb_row = n_per_row / bs, nb_mat = nrow * nb_row, nunits = nmat * nb_mat;
+    const int64_t nb_row = n_per_row / bs, nb_mat = nrow * nb_row, nunits = nmat * nb_mat, rows = nmat * nrow;
     const QParams p = params_for(type, d_raw, d_dst, nunits, d_imatrix, nb_mat, nb_row, 1);
-    if (!dispatch(type, src, p, (hipStream_t)stream)) return 0;
+    if (rowsig_type(type) && d_imatrix) {
+        // the rows' sigma2 in a stream-ordered allocation, released on the stream after the launch (not under
+        // capture: the allocation would become part of the graph)
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cs) != hipSuccess) return 0;
+        if (cs != hipStreamCaptureStatusNone) {
+            fprintf(stderr, "gpuq_requantize_dev: Q4_0 / Q5_0 / Q5_1 with an imatrix refused under stream capture\n");
+            return 0;
+        }
+        void *sig = nullptr;
+        if (hipMallocAsync(&sig, (size_t)rows * 4, st) != hipSuccess) return 0;
+        const bool ok = launch_rows(type, src, p, rows, n_per_row, (float *)sig, st);
+        if (hipFreeAsync(sig, st) != hipSuccess || !ok) return 0;
+    } else if (!launch_rows(type, src, p, rows, n_per_row, nullptr, st)) {
+        return 0;
+    }
     return (size_t)nunits * gpuq_block_bytes(type);
 }
 

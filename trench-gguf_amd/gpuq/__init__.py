@@ -13,10 +13,12 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 F32, F16, Q8_0, BF16, MXFP4 = 0, 1, 8, 30, 39
 Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 10, 11, 12, 13, 14
 IQ2_XXS, IQ2_XS, IQ3_XXS, IQ1_S, IQ4_NL, IQ3_S, IQ2_S, IQ4_XS, IQ1_M = 16, 17, 18, 19, 20, 21, 22, 23, 29
+Q4_0, Q5_0, Q5_1 = 2, 6, 7          # (with F16: llama-quantize's fallback types for rows of other lengths)
 TYPE_NAMES = {Q8_0: "Q8_0", Q2_K: "Q2_K", Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K",
               IQ2_XXS: "IQ2_XXS", IQ2_XS: "IQ2_XS", IQ3_XXS: "IQ3_XXS", IQ1_S: "IQ1_S", IQ4_NL: "IQ4_NL",
-              IQ3_S: "IQ3_S", IQ2_S: "IQ2_S", IQ4_XS: "IQ4_XS", IQ1_M: "IQ1_M"}
-BLOCK = {t: (32 if t in (Q8_0, IQ4_NL) else 256) for t in TYPE_NAMES}
+              IQ3_S: "IQ3_S", IQ2_S: "IQ2_S", IQ4_XS: "IQ4_XS", IQ1_M: "IQ1_M",
+              Q4_0: "Q4_0", Q5_0: "Q5_0", Q5_1: "Q5_1", F16: "F16"}
+BLOCK = {t: (1 if t == F16 else 32 if t in (Q8_0, IQ4_NL, Q4_0, Q5_0, Q5_1) else 256) for t in TYPE_NAMES}
 
 _i, _i64, _sz, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p
 

@@ -24,9 +24,13 @@ part of this repository) and carries a mark that makes libgpuq refuse those type
 grid indices against ggml's own grids. This flag lifts that refusal for test runs. A gpuq_tables.bin written from
 ggml by the reference's gpuq_tables.c needs no flag.
 
-Not here (the reference's other paths): --dump / --dense-dump Hessians, --sub, the CPU quantizer, sources in other
-stored types and the fallback types that libgpuq does not produce (Q4_0, Q5_0, Q5_1, F16). A tensor that needs one
-of these stops the run with its name and the reason; nothing falls back to the CPU.
+llama-quantize's fallback types for rows that are not whole blocks of the asked type (Q4_0, Q5_0, Q5_1, IQ4_NL, Q8_0,
+F16: FALLBACK below) are quantized by libgpuq too, with the tensor's imatrix where ggml takes one; the reference writes
+these through ggml on the CPU (tools/requant_experts.py:732-747).
+
+Not here (the reference's other paths): --dump / --dense-dump Hessians, --sub, the CPU quantizer and sources in other
+stored types. A tensor that needs one of these stops the run with its name and the reason; nothing falls back to the
+CPU.
 """
 import os
 import re
