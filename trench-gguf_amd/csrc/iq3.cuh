@@ -4,8 +4,9 @@
 // (gpuq/gpuq.hip:971-1283). Per lane: one 32-weight sub-block of eight 4-value groups. The whole 4096-entry 3-bit
 // key map (every key is reachable: levels 0..7; off-grid entries packed with their list's offset and length) and the
 // grid (uint32 points, byte i = 2l+1) sit in LDS; neighbour lists stay in HBM. A group's levels are kept as its
-// point's 4 bytes, one dword a group. The neighbour searches are wave-wide (coop.cuh): a trial's 8 groups in two
-// calls of 4 lists a lane, each list with its own staged values.
+// point's 4 bytes, one dword a group. The neighbour searches are wave-wide (coop.cuh): two trials' 8 groups in two
+// calls of 8 lists a lane (a half's 4 groups at both scales, its groups' values staged once), the final pass in two
+// calls of 4; one 8-wave workgroup a CU (the 8-list workspace).
 #pragma once
 #include "iq2.cuh"
 
@@ -71,6 +72,9 @@ DEV int group_key8(const float *xv, float id) {
 }
 
 using Iq3WS = CoopWSM<4, 8, true>;
+// two trials a call: list m = t*4 + k (trial t, group k of the half), the half's 4 groups staged once (rows k), one
+// scale row a trial
+using Iq3WS2 = CoopWSM<8, 8, true, 4, 2>;
 constexpr int IQ3_CH = 4;       // the neighbour search's piece size (candidates a round)
 
 // The 8 groups' points of every lane at one scale (all lanes call it together): a group with act[k] takes the grid
@@ -115,11 +119,54 @@ DEV void iq3_points(const bool (&act)[8], float id, float scale, const float (&x
     }
 }
 
+// the 8 groups' points of every lane at two scales (trial 1 only where `two`), as iq3_points: per half of the groups
+// one call of 8 lists a lane
+template <int GRID>
+DEV void iq3_points2(const bool (&act)[8], const float (&id)[2], const float (&scale)[2], bool two,
+                     const float (&xval)[32], const float (&waux)[32], const int32_t *map, const uint32_t *grid,
+                     const QParams &p, Iq3WS2 &ws, uint32_t (&P)[2][8], bool (&og)[2][8]) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        int mk[8], cnt[8], off[8], gi[8];
+        float sc[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int t = e >> 2, k = 4 * h + (e & 3);
+            const bool a = act[k] && (t == 0 || two);
+            mk[e] = a ? map[group_key8(xval + 4 * k, id[t])] : 0;
+            const bool srch = a && mk[e] < 0;
+            cnt[e] = srch ? m3_cnt(mk[e]) : 0;
+            off[e] = srch ? m3_off(mk[e]) : 0;
+            sc[e] = scale[t];
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+            coop_stage<4>(ws, xval + 4 * (4 * h + m), waux + 4 * (4 * h + m), m * 64 + lane_id());
+        coop_search_m<8, IQ3_CH>(cnt, off, sc, p.neigh, p.neigh_len, ws, EvalIq4{grid}, gi);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int t = e >> 2, k = 4 * h + (e & 3);
+            if (!act[k] || !(t == 0 || two)) continue;
+            og[t][k] = mk[e] >= 0;
+            int g = mk[e];
+            if (g < 0) {
+                g = gi[e];
+                if (g < 0) {
+                    flag_err(p);
+                    g = 0;
+                }
+            }
+            P[t][k] = grid[g];
+        }
+    }
+}
+
 // the shared IQ3 32-weight search (every lane of the wave runs it: the neighbour searches are wave-wide); returns
 // the sub-block scale, P = its 8 group points, live = not skipped
 template <bool XXS, int GRID>
 DEV float iq3_search(const float (&x)[32], const float (&qv)[32], float sigma2, const QParams &p, const uint8_t *lds,
-                     Iq3WS &ws, uint32_t (&P)[8], uint32_t (&bsg)[4], bool &live) {
+                     Iq3WS2 &ws2, uint32_t (&P)[8], uint32_t (&bsg)[4], bool &live) {
+    Iq3WS &ws = *(Iq3WS *)&ws2;
     const uint32_t *grid = Iq4Tab<GRID>::grid(lds);
     const int32_t *map = Iq4Tab<GRID>::map(lds);
     float weight[32], waux[32], xval[32];
@@ -146,21 +193,32 @@ DEV float iq3_search(const float (&x)[32], const float (&qv)[32], float sigma2, 
     }
     constexpr int NT = XXS ? 15 : 9;
 #pragma unroll 1
-    for (int is = -NT; is <= NT; ++is) {
-        const float id = (15 + is * 0.2f) / mx;
-        const float this_scale = 1 / id;
-        uint32_t Pa[8];
-        bool og[8];
+    for (int is = -NT; is <= NT; is += 2) {            // two trials a call (the last alone)
+        const bool two = is + 1 <= NT;
+        float id[2], this_scale[2];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) { Pa[k] = 0x01010101u; og[k] = false; }
-        iq3_points<GRID>(act, id, this_scale, xval, waux, map, grid, p, ws, Pa, og);
-        float sumqx, sumq2;
-        sums_q<32>(weight, xval, Pa, sumqx, sumq2);
-        if (live && sumq2 > 0 && sumqx * sumqx > best * sumq2) {
-            scale = sumqx / sumq2;
-            best = scale * sumqx;
+        for (int t = 0; t < 2; ++t) {
+            id[t] = (15 + (t && two ? is + 1 : is) * 0.2f) / mx;
+            this_scale[t] = 1 / id[t];
+        }
+        uint32_t Pa[2][8];
+        bool og[2][8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) { P[k] = Pa[k]; on_grid[k] = og[k]; }
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int k = 0; k < 8; ++k) { Pa[t][k] = 0x01010101u; og[t][k] = false; }
+        iq3_points2<GRID>(act, id, this_scale, two, xval, waux, map, grid, p, ws2, Pa, og);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            if (t == 1 && !two) break;
+            float sumqx, sumq2;
+            sums_q<32>(weight, xval, Pa[t], sumqx, sumq2);
+            if (live && sumq2 > 0 && sumqx * sumqx > best * sumq2) {
+                scale = sumqx / sumq2;
+                best = scale * sumqx;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) { P[k] = Pa[t][k]; on_grid[k] = og[t][k]; }
+            }
         }
     }
     bool any_off = false;
@@ -189,7 +247,7 @@ DEV float iq3_search(const float (&x)[32], const float (&qv)[32], float sigma2, 
 
 // IQ3_XXS: block d qs[96] = 64 grid bytes, then 8 u32 signs-and-scales (98 bytes)
 struct KIQ3XXS : Iq4Tab<256> {
-    static constexpr int BS = QK, G = 8, N = 32, BB = 98, WS = coop_wsm_bytes<4, 8, true>();
+    static constexpr int BS = QK, G = 8, N = 32, BB = 98, WS = coop_wsm_bytes<8, 8, true, 4, 2>(), WGW = 8;
     static constexpr bool QUEUE = true;         // (tiles of varying cost: the tile queue)
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
                           const QParams &p) {
@@ -201,7 +259,8 @@ struct KIQ3XXS : Iq4Tab<256> {
         const float sigma2 = 2 * grp_chain_sum<G, N>(sq, g) / QK;
         uint32_t P[8], bsg[4];
         bool live;
-        const float scale = iq3_search<true, 256>(x, qv, sigma2, p, lds, *(Iq3WS *)wave_ws<KIQ3XXS>(img), P, bsg, live);
+        const float scale =
+            iq3_search<true, 256>(x, qv, sigma2, p, lds, *(Iq3WS2 *)wave_ws<KIQ3XXS>(img), P, bsg, live);
         const float max_scale = grp_max<G>(live ? scale : 0.f);
         if (!max_scale) return;                               // qs all zero, d = 0
         uint32_t q3lo = 0, q3hi = 0, sas = 0;
@@ -229,7 +288,7 @@ struct KIQ3XXS : Iq4Tab<256> {
 // IQ3_S: block d qs[64] qh[8] signs[32] scales[4] (110 bytes). A skipped (all-zero) sub-block does not advance the
 // qs / signs cursors (ggml's quirk, kept by the reference): the next live sub-block takes its slot.
 struct KIQ3S : Iq4Tab<512> {
-    static constexpr int BS = QK, G = 8, N = 32, BB = 110, WS = coop_wsm_bytes<4, 8, true>();
+    static constexpr int BS = QK, G = 8, N = 32, BB = 110, WS = coop_wsm_bytes<8, 8, true, 4, 2>(), WGW = 8;
     static constexpr bool QUEUE = true;         // (tiles of varying cost: the tile queue)
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
                           const QParams &p) {
@@ -241,7 +300,8 @@ struct KIQ3S : Iq4Tab<512> {
         const float sigma2 = 2 * grp_chain_sum<G, N>(sq, g) / QK;
         uint32_t P[8], bsg[4];
         bool live;
-        const float scale = iq3_search<false, 512>(x, qv, sigma2, p, lds, *(Iq3WS *)wave_ws<KIQ3S>(img), P, bsg, live);
+        const float scale =
+            iq3_search<false, 512>(x, qv, sigma2, p, lds, *(Iq3WS2 *)wave_ws<KIQ3S>(img), P, bsg, live);
         // the slot of this sub-block: the number of live sub-blocks before it
         const uint64_t bal = __ballot(live);
         const int gbase = lane_id() & ~(G - 1);
