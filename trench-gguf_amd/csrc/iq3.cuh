@@ -119,12 +119,13 @@ DEV void iq3_points(const bool (&act)[8], float id, float scale, const float (&x
     }
 }
 
-// the 8 groups' points of every lane at two scales (trial 1 only where `two`), as iq3_points: per half of the groups
-// one call of 8 lists a lane
+// the 8 groups' points of every lane at two scales (trial 1 only where `two`; a lane that is not live searches
+// nothing), as iq3_points: per half of the groups one call of 8 lists a lane. P[t][k]: group k's point at trial t;
+// og: bit 8t + k set where that group's key is on the grid (bits kept in one register, not 16 flags)
 template <int GRID>
-DEV void iq3_points2(const bool (&act)[8], const float (&id)[2], const float (&scale)[2], bool two,
+DEV void iq3_points2(bool live, const float (&id)[2], const float (&scale)[2], bool two,
                      const float (&xval)[32], const float (&waux)[32], const int32_t *map, const uint32_t *grid,
-                     const QParams &p, Iq3WS2 &ws, uint32_t (&P)[2][8], bool (&og)[2][8]) {
+                     const QParams &p, Iq3WS2 &ws, uint32_t (&P)[2][8], uint32_t &og) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         int mk[8], cnt[8], off[8], gi[8];
@@ -132,7 +133,7 @@ DEV void iq3_points2(const bool (&act)[8], const float (&id)[2], const float (&s
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int t = e >> 2, k = 4 * h + (e & 3);
-            const bool a = act[k] && (t == 0 || two);
+            const bool a = live && (t == 0 || two);
             mk[e] = a ? map[group_key8(xval + 4 * k, id[t])] : 0;
             const bool srch = a && mk[e] < 0;
             cnt[e] = srch ? m3_cnt(mk[e]) : 0;
@@ -146,8 +147,8 @@ DEV void iq3_points2(const bool (&act)[8], const float (&id)[2], const float (&s
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int t = e >> 2, k = 4 * h + (e & 3);
-            if (!act[k] || !(t == 0 || two)) continue;
-            og[t][k] = mk[e] >= 0;
+            if (!live || !(t == 0 || two)) continue;
+            if (mk[e] >= 0) og |= 1u << (8 * t + k);
             int g = mk[e];
             if (g < 0) {
                 g = gi[e];
@@ -185,12 +186,8 @@ DEV float iq3_search(const float (&x)[32], const float (&qv)[32], float sigma2, 
     live = XXS ? !(mx < EPS_IQ3XXS) : (mx != 0.f);
     float best = 0;
     float scale = live ? mx / 15 : 0.f;
-    bool on_grid[8], act[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        on_grid[k] = XXS;                                     // (IQ3_S starts from "not on the grid")
-        act[k] = live;
-    }
+    uint32_t on_grid = XXS ? 0xffu : 0u;                  // bit k: group k's point on the grid (IQ3_S starts from
+                                                          // "not on the grid")
     constexpr int NT = XXS ? 15 : 9;
 #pragma unroll 1
     for (int is = -NT; is <= NT; is += 2) {            // two trials a call (the last alone)
@@ -201,13 +198,12 @@ DEV float iq3_search(const float (&x)[32], const float (&qv)[32], float sigma2, 
             id[t] = (15 + (t && two ? is + 1 : is) * 0.2f) / mx;
             this_scale[t] = 1 / id[t];
         }
-        uint32_t Pa[2][8];
-        bool og[2][8];
+        uint32_t Pa[2][8], og = 0;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int k = 0; k < 8; ++k) { Pa[t][k] = 0x01010101u; og[t][k] = false; }
-        iq3_points2<GRID>(act, id, this_scale, two, xval, waux, map, grid, p, ws2, Pa, og);
+            for (int k = 0; k < 8; ++k) Pa[t][k] = 0x01010101u;
+        iq3_points2<GRID>(live, id, this_scale, two, xval, waux, map, grid, p, ws2, Pa, og);
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             if (t == 1 && !two) break;
@@ -217,18 +213,18 @@ DEV float iq3_search(const float (&x)[32], const float (&qv)[32], float sigma2, 
                 scale = sumqx / sumq2;
                 best = scale * sumqx;
 #pragma unroll
-                for (int k = 0; k < 8; ++k) { P[k] = Pa[t][k]; on_grid[k] = og[t][k]; }
+                for (int k = 0; k < 8; ++k) P[k] = Pa[t][k];
+                on_grid = (og >> (8 * t)) & 0xffu;
             }
         }
     }
-    bool any_off = false;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) any_off |= !on_grid[k];
+    const bool any_off = on_grid != 0xffu;
     const bool fin = live && any_off && scale > 0;
     {
         const float id = 1 / scale;
+        bool act[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) act[k] = fin && !(XXS && on_grid[k]);   // (IQ3_S re-searches every group)
+        for (int k = 0; k < 8; ++k) act[k] = fin && !(XXS && ((on_grid >> k) & 1u));   // (IQ3_S: every group)
         bool og[8];
         iq3_points<GRID>(act, id, scale, xval, waux, map, grid, p, ws, P, og);
         if (fin) {
