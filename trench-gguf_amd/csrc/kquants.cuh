@@ -44,14 +44,17 @@ template <int G, int N> DEV void grp_gather(float v, float (&out)[N]) {
 }
 
 // ------------------------------------------------------------------ searches (one lane, one sub-block)
-// make_qp_quants: levels 0..nmax for non-negative x (gpuq/gpuq.hip:114-176); uint8 stores as ggml's
-template <int N> DEV float qp_levels(int nmax, const float (&x)[N], Lv<N> &L, const float (&qw)[N]) {
+// make_qp_quants: levels 0..nmax for non-negative x (gpuq/gpuq.hip:114-176); uint8 stores as ggml's.
+// qp_start: the first scale, the eight trial scales, and the best one's levels and sums (sum w x l, sum w l^2); false
+// for a group whose largest value is below EPS_GROUP (levels 0, scale 0, no refinement)
+template <int N>
+DEV bool qp_start(int nmax, const float (&x)[N], Lv<N> &L, const float (&qw)[N], float &sumlx, float &suml2) {
     float mx = 0;
 #pragma unroll
     for (int i = 0; i < N; ++i) mx = fmax_sel(mx, x[i]);
     if (mx < EPS_GROUP) {
         L.clear();
-        return 0.f;
+        return false;
     }
     float iscale = nmax / mx;
 #pragma unroll
@@ -76,7 +79,8 @@ template <int N> DEV float qp_levels(int nmax, const float (&x)[N], Lv<N> &L, co
         }
         if (mse < best_mse) { best_mse = mse; iscale = iscale_is; }
     }
-    float sumlx = 0, suml2 = 0;
+    sumlx = 0;
+    suml2 = 0;
 #pragma unroll
     for (int i = 0; i < N; ++i) {
         const int l = imin(nmax, nint(iscale * x[i]));
@@ -84,30 +88,50 @@ template <int N> DEV float qp_levels(int nmax, const float (&x)[N], Lv<N> &L, co
         sumlx += qw[i] * x[i] * l;
         suml2 += qw[i] * l * l;
     }
-    for (int pass = 0; pass < 5; ++pass) {
-        int changed = 0;
-#pragma unroll
-        for (int i = 0; i < N; ++i) {
-            const float w = qw[i];
-            const int Li = (int)L.get(i);
-            float slx = sumlx - w * x[i] * Li;
-            float sl2 = suml2 - w * Li * Li;
-            if (slx > 0 && sl2 > 0) {
-                const int nl = imin(nmax, nint(x[i] * sl2 / slx));
-                if (nl != Li) {
-                    slx += w * x[i] * nl;
-                    sl2 += w * nl * nl;
-                    if (slx * slx * suml2 > sumlx * sumlx * sl2) {
-                        L.put(i, (uint32_t)nl);
-                        sumlx = slx;
-                        suml2 = sl2;
-                        ++changed;
-                    }
-                }
-            }
+    return true;
+}
+
+// one element of a refinement pass: element (x, w) at level li against the running sums; true when the pass changes
+// it, to level nl with the sums (nslx, nsl2)
+DEV bool qp_step(int nmax, float x, float w, int li, float sumlx, float suml2, int &nl, float &nslx, float &nsl2) {
+    float slx = sumlx - w * x * li;
+    float sl2 = suml2 - w * li * li;
+    if (slx > 0 && sl2 > 0) {
+        nl = imin(nmax, nint(x * sl2 / slx));
+        if (nl != li) {
+            slx += w * x * nl;
+            sl2 += w * nl * nl;
+            nslx = slx;
+            nsl2 = sl2;
+            return slx * slx * suml2 > sumlx * sumlx * sl2;
         }
-        if (!changed) break;
     }
+    return false;
+}
+
+// one refinement pass over the group in index order; the number of levels it changed
+template <int N>
+DEV int qp_pass(int nmax, const float (&x)[N], Lv<N> &L, const float (&qw)[N], float &sumlx, float &suml2) {
+    int changed = 0;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        int nl = 0;
+        float a = 0.f, b = 0.f;
+        if (qp_step(nmax, x[i], qw[i], (int)L.get(i), sumlx, suml2, nl, a, b)) {
+            L.put(i, (uint32_t)nl);
+            sumlx = a;
+            suml2 = b;
+            ++changed;
+        }
+    }
+    return changed;
+}
+
+template <int N> DEV float qp_levels(int nmax, const float (&x)[N], Lv<N> &L, const float (&qw)[N]) {
+    float sumlx, suml2;
+    if (!qp_start<N>(nmax, x, L, qw, sumlx, suml2)) return 0.f;
+    for (int pass = 0; pass < 5; ++pass)
+        if (!qp_pass<N>(nmax, x, L, qw, sumlx, suml2)) break;
     return suml2 > 0.0f ? sumlx / suml2 : 0.0f;
 }
 
@@ -163,30 +187,8 @@ template <int G> DEV float qp_levels_grp(int nmax, const float (&x)[G], Lv<G> &L
         sumlx += qw[i] * x[i] * l;
         suml2 += qw[i] * l * l;
     }
-    for (int pass = 0; pass < 5; ++pass) {
-        int changed = 0;
-#pragma unroll
-        for (int i = 0; i < G; ++i) {
-            const float w = qw[i];
-            const int Li = (int)L.get(i);
-            float slx = sumlx - w * x[i] * Li;
-            float sl2 = suml2 - w * Li * Li;
-            if (slx > 0 && sl2 > 0) {
-                const int nl = imin(nmax, nint(x[i] * sl2 / slx));
-                if (nl != Li) {
-                    slx += w * x[i] * nl;
-                    sl2 += w * nl * nl;
-                    if (slx * slx * suml2 > sumlx * sumlx * sl2) {
-                        L.put(i, (uint32_t)nl);
-                        sumlx = slx;
-                        suml2 = sl2;
-                        ++changed;
-                    }
-                }
-            }
-        }
-        if (!changed) break;
-    }
+    for (int pass = 0; pass < 5; ++pass)
+        if (!qp_pass<G>(nmax, x, L, qw, sumlx, suml2)) break;
     return suml2 > 0.0f ? sumlx / suml2 : 0.0f;
 }
 
