@@ -2,6 +2,7 @@
 """bench.py - throughput of the MI355X GGUF quantizer on the configured synthetic workloads.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-host] [--only NAME,...] [--experts N]
+    python bench.py --only experts16      (not in the default run: five search types on 16 BF16 experts)
 
 One "step" is one pass of the quantizer over one workload tensor already resident in HBM (the device entry point
 gpuq_requantize_dev: source bytes decoded in registers, quantized, blocks written to HBM). The headline line is
@@ -10,7 +11,10 @@ log-normal(0, 1.5) imatrix a expert). `per_type` adds Q8_0 on a 4096 x 4096 F32 
 and ramp time no longer weigh), Q4_K and Q6_K on a
 2048 x 7168 BF16 tensor (N(0, 0.02) plus 0.1% outliers at +-8 sigma, a log-normal imatrix), IQ1_S / IQ1_M on 384 x
 2048 x 7168 MXFP4 experts and IQ2_S with LDLQ error feedback on 64 BF16 experts; `other_types` the remaining nine
-types on the 2048 x 7168 tensor (GPU rate, roofline, byte spot check on 64 rows). Kernel time comes from HIP events
+types on the 2048 x 7168 tensor (GPU rate, roofline, byte spot check on 64 rows). `--only experts16` runs Q3_K,
+IQ2_XS, IQ2_S, IQ3_XXS and IQ3_S on 16 of the BF16 experts: launches long enough that neither the tile queue's last
+round (that tensor gives 2,048 resident waves 3.5 tiles each) nor the write-back of each resident wave's register
+spill area, once a launch, weighs on the rate or the traffic. Kernel time comes from HIP events
 on the launch stream; inputs that fit the 256 MB Infinity Cache are rotated over enough copies that every launch
 reads HBM.
 
@@ -44,8 +48,9 @@ VALU_PEAK_TOPS = 78.6          # 157.3 TFLOP/s FP32 vector / 2 flops an FMA: 2 w
 FP64_PEAK_TFLOPS = 78.6        # MI355X FP64 (vector and matrix)
 MALL_BYTES = 256 << 20         # Infinity Cache
 CPU_MIN_S = 10.0               # the CPU baseline repeats its sample until this much CPU time has run
-ENTRIES = ["IQ2_XXS", "Q8_0", "Q8_0_large", "Q4_K", "Q6_K", "IQ1_S", "IQ1_M", "LDLQ", "other"]
+ENTRIES = ["IQ2_XXS", "Q8_0", "Q8_0_large", "Q4_K", "Q6_K", "IQ1_S", "IQ1_M", "LDLQ", "other", "experts16"]
 OTHER = ["Q2_K", "Q3_K", "Q5_K", "IQ4_NL", "IQ4_XS", "IQ2_XS", "IQ2_S", "IQ3_XXS", "IQ3_S"]
+EXPERTS16 = ["Q3_K", "IQ2_XS", "IQ2_S", "IQ3_XXS", "IQ3_S"]     # (run only when asked for: --only experts16)
 
 
 def log(msg):
@@ -601,6 +606,15 @@ def main():
                 per[name], _ = type_entry(torch, gq, gpuq, orc, orc_ops, c4, getattr(gpuq, name), ksteps, 1, srows,
                                           want_cpu)
         del c4
+        torch.cuda.empty_cache()
+    if "experts16" in only:
+        c16 = wl_c3(torch, gpuq, 16)
+        for name in EXPERTS16:
+            log("experts16: %s on %s" % (name, c16.name))
+            e, out = type_entry(torch, gq, gpuq, orc, orc_ops, c16, getattr(gpuq, name), ksteps, 1, 64, False)
+            per["%s_16_experts" % name] = e
+            del out
+        del c16
         torch.cuda.empty_cache()
     if want("LDLQ"):
         log("per type: IQ2_S LDLQ")
