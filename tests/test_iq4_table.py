@@ -74,3 +74,29 @@ def test_table_lookup_equals_reference_search():
     idx = np.random.default_rng(4).integers(0, x.size, 20000)
     xs = np.concatenate([x[idx], np.array([np.nan, -np.inf, np.inf], dtype=np.float32)])
     assert np.array_equal(reference(xs), table_index(xs))
+
+
+def value_table(x):
+    """the trial passes' lookup (iq4_value): floor(x) + 135 into a table of each interval's two ends (the upper equal
+    to the lower for the last interval), the nearer end by x - lo < hi - x; for finite x with floor(x) in [-135, 134]"""
+    t = np.arange(-135, 135, dtype=np.float32)
+    ml_t = np.array([max([j for j in range(16) if KV[j] <= v] or [0]) for v in t])
+    lo_t, hi_t = KV[ml_t], KV[np.minimum(ml_t + 1, 15)]
+    fi = np.floor(x).astype(np.int64) + 135
+    lo, hi = lo_t[fi], hi_t[fi]
+    return np.where((x - lo).astype(np.float32) < (hi - x).astype(np.float32), lo, hi)
+
+
+def test_value_table_equals_reference_search_value():
+    """the codebook value of the trials' lookup equals kv[best_index_int8(x)] wherever a trial can ask for it: every
+    finite x with |x| <= 134.0001 (a trial's |id x| stays within 134 (1 + 2^-24)^2)"""
+    x = sample()
+    x = x[np.isfinite(x) & (np.abs(x) <= np.float32(134.0001))]
+    lim = np.float32(np.nextafter(np.float32(135), np.float32(0)))
+    edge = np.array([-134.0001, -134, -128.5, -127.5, -127, -115.5, 113, 113.5, 120, 134, 134.0001, lim, -lim],
+                    dtype=np.float32)
+    x = np.concatenate([x, edge[np.abs(edge) <= np.float32(134.0001)]])
+    assert x.size > 100000
+    want = KV[table_index(x)]
+    got = value_table(x)
+    assert np.array_equal(got, want), int((got != want).sum())

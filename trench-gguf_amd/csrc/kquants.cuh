@@ -890,7 +890,17 @@ DEV int iq4_index(float x, const Iq4Ent *tab, float &q) {
     q = down ? e.lo : hi;
     return down ? ml : ml + 1;
 }
-// the table (and the 16 codebook values before it), staged by a workgroup's threads
+// The trial scales' codebook value alone (their levels are not kept), for finite x with floor(x) in [-135, 134]
+// (a trial's |id x| <= 134: |id| <= 134 / max|x|): a second table, indexed by floor(x) + 135, holds the interval's two
+// ends as floats, the upper one equal to the lower for the last interval (x >= kv[15], where the search keeps kv[15],
+// and below kv[0] the first interval's ends); the nearer end by the same test x - lo < hi - x, which for equal ends
+// gives that end.
+constexpr int IQ4_Q0 = -135, IQ4_QN = 134 - IQ4_Q0 + 1;
+DEV float iq4_value(float x, const float2 *tq) {
+    const float2 e = tq[(int)floorf(x) - IQ4_Q0];
+    return x - e.x < e.y - x ? e.x : e.y;
+}
+// the tables (and the 16 codebook values before them), staged by a workgroup's threads
 DEV void iq4_stage(uint8_t *lds) {
     float *kv = (float *)lds;
     if (threadIdx.x < 16) kv[threadIdx.x] = k_iq4f[threadIdx.x];
@@ -902,13 +912,22 @@ DEV void iq4_stage(uint8_t *lds) {
         for (int j = 1; j < 16; ++j) ml = k_iq4f[j] <= v ? j : ml;
         tab[i] = Iq4Ent{k_iq4f[ml], ml + 256 * (int)k_iq4f[ml < 15 ? ml + 1 : 15]};
     }
+    float2 *tq = (float2 *)(lds + 64 + IQ4_TN * (int)sizeof(Iq4Ent));
+    for (int i = threadIdx.x; i < IQ4_QN; i += blockDim.x) {
+        const float v = (float)(i + IQ4_Q0);
+        int ml = 0;
+#pragma unroll
+        for (int j = 1; j < 16; ++j) ml = k_iq4f[j] <= v ? j : ml;
+        tq[i] = make_float2(k_iq4f[ml], k_iq4f[ml < 15 ? ml + 1 : 15]);
+    }
 }
-constexpr int IQ4_TAB = 64 + IQ4_TN * (int)sizeof(Iq4Ent);
+constexpr int IQ4_TAB = 64 + IQ4_TN * (int)sizeof(Iq4Ent) + IQ4_QN * 8;
 DEV const Iq4Ent *iq4_tab(const uint8_t *lds) { return (const Iq4Ent *)(lds + 64); }
+DEV const float2 *iq4_qtab(const uint8_t *lds) { return (const float2 *)(lds + 64 + IQ4_TN * (int)sizeof(Iq4Ent)); }
 
 // one 32-weight sub-block's scale search; fills Lb, returns the scale (0 for a negligible block)
 DEV float iq4_block(const float (&xb)[32], const float (&weight)[32], Lv<32> &Lb, const float *kv,
-                    const Iq4Ent *tab) {
+                    const Iq4Ent *tab, const float2 *tq) {
     float amax = 0, mx = 0;
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
@@ -931,7 +950,28 @@ DEV float iq4_block(const float (&xb)[32], const float (&weight)[32], Lv<32> &Lb
     }
     d = sumq2 > 0 ? sumqx / sumq2 : 0.f;
     float best = d * sumqx;
-    for (int itry = -7; itry <= 7; ++itry) {
+    bool fin = true;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) fin = fin && __builtin_isfinite(xb[j]);
+    if (fin) {
+        for (int itry = -7; itry <= 7; ++itry) {
+            id = (float)(itry + (-127)) / mx;
+            sumqx = sumq2 = 0;
+#pragma unroll
+            for (int j = 0; j < 32; ++j) {
+                const float q = iq4_value(id * xb[j], tq);
+                const float w = weight[j];
+                sumqx += w * q * xb[j];
+                sumq2 += w * q * q;
+            }
+            if (sumq2 > 0 && sumqx * sumqx > best * sumq2) {
+                d = sumqx / sumq2;
+                best = d * sumqx;
+            }
+        }
+        return d;
+    }
+    for (int itry = -7; itry <= 7; ++itry) {            // (a non-finite value: the clamped lookup)
         id = (float)(itry + (-127)) / mx;
         sumqx = sumq2 = 0;
 #pragma unroll
@@ -975,7 +1015,7 @@ struct KIQ4XS {
         }
         Lv<32> Lb;
         Lb.clear();
-        const float sd = iq4_block(x, weight, Lb, kv, iq4_tab(lds));
+        const float sd = iq4_block(x, weight, Lb, kv, iq4_tab(lds), iq4_qtab(lds));
         const int jm = grp_argmax_first<G>(fabsf(sd), g);
         const float amax_scale = grp_bcast<G>(fabsf(sd), jm);
         const float max_scale = amax_scale > 0 ? grp_bcast<G>(sd, jm) : 0.f;   // (+0 when no |d| beat 0)
@@ -1022,7 +1062,7 @@ struct KIQ4NL {
         }
         Lv<32> Lb;
         Lb.clear();
-        const float s = iq4_block(x, weight, Lb, kv, iq4_tab(lds));
+        const float s = iq4_block(x, weight, Lb, kv, iq4_tab(lds), iq4_qtab(lds));
         img_or16(img, boff, f2h(s));
         const float id = s ? 1 / s : 0;
 #pragma unroll
