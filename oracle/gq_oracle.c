@@ -1231,12 +1231,14 @@ static void o_iq3_s(const float *xbl, const float *qwbl, uint8_t *y, const otab 
 static const int8_t k_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
 
 /* index of the nearest codebook value, the lower one on ties away from it (gpuq/gpuq.hip:1286-1295) */
-static int nearest_iq4(float x) {
+static int nearest_iq4(float x, int value_only) {
     /* charged as the table form (the interval kv[ml] <= x < kv[ml+1] read from a table indexed by floor(x), the
      * codebook values being integers): floor, clamp, NaN select, conversion, then the two differences, their
-     * compare and two selects; the bisection below gives the same index (tests/test_iq4_table.py) */
+     * compare and two selects; where only the value is used (the trial scales, whose |x| stays within the table for
+     * finite values) floor, conversion, the two differences, their compare and one select. The bisection below gives
+     * the same index (tests/test_iq4_table.py) */
     const int8_t *val = k_iq4nl;
-    OPS(9);
+    OPS(value_only ? 6 : 9);
     if (x <= val[0]) return 0;
     if (x >= val[15]) return 15;
     int lo = 0, hi = 15;
@@ -1282,7 +1284,7 @@ static void iq4_impl(int SB, const float *x, uint8_t *dh, uint8_t *q4, uint16_t 
         float sumqx = 0, sumq2 = 0;
         for (int j = 0; j < bsz; ++j) {
             const float al = id * xb[j];
-            const int l = nearest_iq4(al);
+            const int l = nearest_iq4(al, 0);
             Lb[j] = (uint8_t)l;
             const float q = k_iq4nl[l];
             const float w = weight[j];
@@ -1297,7 +1299,7 @@ static void iq4_impl(int SB, const float *x, uint8_t *dh, uint8_t *q4, uint16_t 
             sumqx = sumq2 = 0;
             for (int j = 0; j < bsz; ++j) {
                 const float al = id * xb[j];
-                const int l = nearest_iq4(al);
+                const int l = nearest_iq4(al, 1);
                 const float q = k_iq4nl[l];
                 const float w = weight[j];
                 sumqx += w * q * xb[j];
@@ -1328,7 +1330,7 @@ static void iq4_impl(int SB, const float *x, uint8_t *dh, uint8_t *q4, uint16_t 
             const float idl = dl ? 1 / dl : 0.f;
             uint8_t *Lb = L + ib * bsz;
             const float *xb = x + ib * bsz;
-            for (int j = 0; j < bsz; ++j) Lb[j] = (uint8_t)nearest_iq4(idl * xb[j]);
+            for (int j = 0; j < bsz; ++j) Lb[j] = (uint8_t)nearest_iq4(idl * xb[j], 0);
             OPS(6 + C_DIV + bsz);
             l += 32;
             const uint8_t l_l = (uint8_t)(l & 0xf);
@@ -1340,7 +1342,7 @@ static void iq4_impl(int SB, const float *x, uint8_t *dh, uint8_t *q4, uint16_t 
     } else {
         put16(dh, f32_to_f16(scales[0]));
         const float id = scales[0] ? 1 / scales[0] : 0;
-        for (int j = 0; j < SB; ++j) L[j] = (uint8_t)nearest_iq4(id * x[j]);
+        for (int j = 0; j < SB; ++j) L[j] = (uint8_t)nearest_iq4(id * x[j], 0);
         OPS(C_DIV + SB);
     }
     for (int i = 0; i < SB / 32; ++i)
