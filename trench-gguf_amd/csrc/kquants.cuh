@@ -994,7 +994,7 @@ DEV float iq4_block(const float (&xb)[32], const float (&weight)[32], Lv<32> &Lb
 // IQ4_XS: block d scales_h scales_l[4] qs[128] (136 bytes); lane g = sub-block g
 struct KIQ4XS {
     static constexpr int BS = QK, G = 8, N = 32, BB = 136, TAB = IQ4_TAB;
-    static constexpr int WPE = 3;    // three waves a SIMD (168 VGPRs, no spill with the 8-byte table entries)
+    static constexpr int WPE = 3;    // three waves a SIMD (at most 168 VGPRs, no spill with the 8-byte table entries)
     static DEV void stage(const QParams &, uint8_t *lds) { iq4_stage(lds); }
     static DEV void quant(const float (&x)[N], const float *qwp, int g, uint8_t *img, int boff, uint8_t *lds,
                           const QParams &) {
