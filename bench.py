@@ -10,7 +10,8 @@ IQ2_XXS with imatrix on 256 stacked BF16 experts of 2048 x 7168 (expert e ~ N(0,
 log-normal(0, 1.5) imatrix a expert). `per_type` adds Q8_0 on a 4096 x 4096 F32 tensor (and on 64 of them, 4.3 GB, where launch
 and ramp time no longer weigh), Q4_K and Q6_K on a
 2048 x 7168 BF16 tensor (N(0, 0.02) plus 0.1% outliers at +-8 sigma, a log-normal imatrix), IQ1_S / IQ1_M on 384 x
-2048 x 7168 MXFP4 experts and IQ2_S with LDLQ error feedback on 64 BF16 experts; `other_types` the remaining nine
+2048 x 7168 MXFP4 experts, IQ2_S with LDLQ error feedback on 64 BF16 experts, and ggml's to_float of the headline's own
+IQ2_XXS blocks (gpuq_dequantize_dev, 16 experts' worth, HBM-bound); `other_types` the remaining nine
 types on the 2048 x 7168 tensor (GPU rate, roofline, byte spot check on 64 rows). `--only experts16` runs Q3_K,
 IQ2_XS, IQ2_S, IQ3_XXS and IQ3_S on 16 of the BF16 experts: launches long enough that neither the tile queue's last
 round (that tensor gives 2,048 resident waves 3.5 tiles each) nor the write-back of each resident wave's register
@@ -354,6 +355,46 @@ def time_gpu(torch, gq, gpuq, wl, typ, steps, warmup):
     return ms, result
 
 
+def bench_to_float(torch, gq, gpuq, orc, q, typ, nblk, steps, warmup):
+    """gpuq_dequantize_dev (ggml's to_float) over nblk blocks already in HBM (the quantizer's own output), HIP events
+    on the launch stream: HBM bytes (blocks read, f32 written) against 8 TB/s and a device copy of as many bytes; the
+    first 64 blocks' values against the oracle's to_float, bit for bit"""
+    bb = gq.gpuq_block_bytes(typ)
+    qv = q[: nblk * bb]
+    outs = [torch.empty(nblk * 256, dtype=torch.float32, device="cuda") for _ in range(2)]
+    stream = torch.cuda.current_stream()
+
+    def launch(i):
+        if gq.gpuq_dequantize_dev(typ, qv.data_ptr(), outs[i % 2].data_ptr(), nblk, stream.cuda_stream) != nblk * 1024:
+            raise RuntimeError("gpuq_dequantize_dev failed for %s" % gpuq.TYPE_NAMES[typ])
+
+    for i in range(warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    hold_gpu(torch, 2.0 + 0.05 * steps)
+    e0.record(stream)
+    for i in range(steps):
+        launch(warmup + i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    got = outs[(warmup + steps - 1) % 2][: 64 * 256].cpu().numpy()
+    want = orc.dequantize(typ, qv[: 64 * bb].cpu().numpy(), 64 * 256)
+    nbytes = nblk * bb + nblk * 256 * 4
+    achieved = nbytes / (ms / 1e3) / 1e9
+    copy_gbs = copy_reference(torch, nbytes)
+    return {"workload": "%s blocks of %d BF16 experts of 2048x7168 (the headline's output) -> f32" %
+                        (gpuq.TYPE_NAMES[typ], nblk // (2048 * 7168 // 256)),
+            "entry_point": "gpuq_dequantize_dev", "value": round(nblk * 256 / (ms / 1e3) / 1e6, 1),
+            "unit": "Mweights/s", "ms_per_step": round(ms, 4), "steps": steps,
+            "sample_identical_to_oracle": bool(np.array_equal(got.view(np.uint32), want.view(np.uint32))),
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes,
+                         "device_copy_same_bytes_GBps": round(copy_gbs, 1),
+                         "frac_of_device_copy": round(achieved / copy_gbs, 4)}}
+
+
 def copy_reference(torch, total_bytes, steps=20):
     """GB/s of a torch device copy that moves `total_bytes` (half read, half written), timed as time_gpu times a
     kernel (HIP events, sources rotated past the Infinity Cache): what a plain streaming kernel of that size reaches"""
@@ -558,6 +599,10 @@ def main():
         if not args.no_host:
             log("host entry point: IQ2_XXS on 16 experts")
             host["IQ2_XXS"] = host_api(torch, gq, gpuq, c3, gpuq.IQ2_XXS, min(16, c3.nmat), out)
+        nblk16 = min(16, c3.nmat) * (2048 * 7168 // 256)
+        log("to_float: IQ2_XXS blocks of %d experts" % (nblk16 // (2048 * 7168 // 256)))
+        per["IQ2_XXS_to_float"] = bench_to_float(torch, gq, gpuq, orc, out, gpuq.IQ2_XXS, nblk16, args.steps,
+                                                 args.warmup)
         del c3, out
         torch.cuda.empty_cache()
     if want("Q8_0"):

@@ -6,7 +6,7 @@
 // produces one 32-value chunk (8 threads a super-block) with 16-byte stores; the dequantizer grid (uint64 points) is
 // read through the cache.
 #pragma once
-#include "common.cuh"
+#include "frame.cuh"
 
 DEV uint32_t ksigns7(uint32_t k) { return k | ((uint32_t)(__popc(k) & 1) << 7); }
 DEV float sgnb(uint32_t s, int j) { return (s >> j) & 1 ? -1.f : 1.f; }
@@ -203,26 +203,49 @@ template <int TYPE> DEV void dq_chunk(const uint8_t *x, int ib, float (&y)[32], 
     }
 }
 
+// A wave's 64 threads each decode 32 consecutive values (thread t: values 32t .. 32t+31 of the launch), so the wave's
+// output is one contiguous run of 2,048 floats. Written straight from the threads, each 16-byte store instruction
+// would touch 64 lines 128 bytes apart; the values go through the wave's LDS rows instead (a thread's eight float4
+// 144 bytes apart: a quarter-wave's 16-byte writes fall in distinct banks) and leave as eight stores of 1 KB runs.
+// n32: the launch's 32-value units; a unit past it is neither read nor written.
+DEV void store_runs(float4 *st, float *out, int64_t t, int64_t n32, const float (&y)[32]) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st[lane * 9 + i] = make_float4(y[4 * i], y[4 * i + 1], y[4 * i + 2], y[4 * i + 3]);
+    wave_sync();
+    const int64_t t0 = t - lane;                        // the wave's first unit
+    float4 *o = (float4 *)(out + t0 * 32);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int f = lane + 64 * i;                    // float4 f of the wave's run: unit f / 8, part f % 8
+        if (t0 + f / 8 < n32) o[f] = st[(f / 8) * 9 + f % 8];
+    }
+}
+
 template <int TYPE, int BB>
 __global__ __launch_bounds__(256) void k_dequant(const uint8_t *q, float *out, int64_t nblocks, const uint64_t *grid) {
+    __shared__ float4 st[4][64 * 9];
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= nblocks * 8) return;
-    const int64_t b = t / 8;
-    const int ib = (int)(t % 8);
     float y[32];
-    dq_chunk<TYPE>(q + b * BB, ib, y, grid);
-    float4 *o = (float4 *)(out + b * QK + 32 * ib);
+    if (t < nblocks * 8) {
+        dq_chunk<TYPE>(q + (t / 8) * BB, (int)(t % 8), y, grid);
+    } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = make_float4(y[4 * i], y[4 * i + 1], y[4 * i + 2], y[4 * i + 3]);
+        for (int i = 0; i < 32; ++i) y[i] = 0.f;
+    }
+    store_runs(st[threadIdx.x >> 6], out, t, nblocks * 8, y);
 }
 
 // source bytes -> f32, one thread a 32-value block (gpuq/gpuq.hip:2123-2141)
 template <int SRC> __global__ __launch_bounds__(256) void k_decode(const uint8_t *in, float *out, int64_t nblk) {
+    __shared__ float4 st[4][64 * 9];
     const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= nblk) return;
     float v[32];
-    SrcLoad<SRC, 32>::load(in, b * 32, v);
-    float4 *o = (float4 *)(out + b * 32);
+    if (b < nblk) {
+        SrcLoad<SRC, 32>::load(in, b * 32, v);
+    } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+        for (int i = 0; i < 32; ++i) v[i] = 0.f;
+    }
+    store_runs(st[threadIdx.x >> 6], out, b, nblk, v);
 }
