@@ -361,11 +361,15 @@ def bench_to_float(torch, gq, gpuq, orc, q, typ, nblk, steps, warmup):
     first 64 blocks' values against the oracle's to_float, bit for bit"""
     bb = gq.gpuq_block_bytes(typ)
     qv = q[: nblk * bb]
+    # the blocks rotated over copies (twice the 256 MB Infinity Cache between two reads of one copy), so every launch
+    # reads them from HBM as the output goes to it
+    srcs = [qv] + [qv.clone() for _ in range(max(0, -(-2 * MALL_BYTES // (nblk * bb)) - 1))]
     outs = [torch.empty(nblk * 256, dtype=torch.float32, device="cuda") for _ in range(2)]
     stream = torch.cuda.current_stream()
 
     def launch(i):
-        if gq.gpuq_dequantize_dev(typ, qv.data_ptr(), outs[i % 2].data_ptr(), nblk, stream.cuda_stream) != nblk * 1024:
+        src = srcs[i % len(srcs)]
+        if gq.gpuq_dequantize_dev(typ, src.data_ptr(), outs[i % 2].data_ptr(), nblk, stream.cuda_stream) != nblk * 1024:
             raise RuntimeError("gpuq_dequantize_dev failed for %s" % gpuq.TYPE_NAMES[typ])
 
     for i in range(warmup):
@@ -387,10 +391,11 @@ def bench_to_float(torch, gq, gpuq, orc, q, typ, nblk, steps, warmup):
     return {"workload": "%s blocks of %d BF16 experts of 2048x7168 (the headline's output) -> f32" %
                         (gpuq.TYPE_NAMES[typ], nblk // (2048 * 7168 // 256)),
             "entry_point": "gpuq_dequantize_dev", "value": round(nblk * 256 / (ms / 1e3) / 1e6, 1),
-            "unit": "Mweights/s", "ms_per_step": round(ms, 4), "steps": steps,
+            "unit": "Mweights/s", "ms_per_step": round(ms, 4), "steps": steps, "source_copies": len(srcs),
             "sample_identical_to_oracle": bool(np.array_equal(got.view(np.uint32), want.view(np.uint32))),
             "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(achieved / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes,
+                         "traffic": pmc_traffic("IQ2_XXS to_float 16x2048x7168"),
                          "device_copy_same_bytes_GBps": round(copy_gbs, 1),
                          "frac_of_device_copy": round(achieved / copy_gbs, 4)}}
 
