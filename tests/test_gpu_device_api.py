@@ -85,6 +85,56 @@ def test_dequantize_src_dev_matches_oracle(env, oracle_lib, src):
     assert np.array_equal(d_out.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
+GUARD = 4096        # floats after the output that no launch may write
+
+
+@pytest.mark.parametrize("typ", [16, 12], ids=["iq2_xxs", "q4_k"])
+def test_dequantize_dev_ragged_counts(env, oracle_lib, typ):
+    """block counts that end inside a wave (8 blocks a wave) and inside a workgroup (32): every value bit for bit,
+    and the floats after the last block untouched (a wave's stores stop at the launch's last block)"""
+    torch, gq = env
+    rng = np.random.default_rng(typ + 31)
+    x = (rng.standard_normal((1, 41 * 256)) * 0.02).astype(np.float32)
+    im = rng.lognormal(0.0, 1.5, 41 * 256).astype(np.float32)
+    q = oracle_lib.quantize(typ, x, im).reshape(-1)
+    bb = gq.gpuq_block_bytes(typ)
+    d_q = torch.from_numpy(q).cuda()
+    st = torch.cuda.current_stream().cuda_stream
+    for nblk in (1, 3, 9, 33, 41):
+        want = oracle_lib.dequantize(typ, np.ascontiguousarray(q[: nblk * bb]), nblk * 256)
+        d_out = torch.full((nblk * 256 + GUARD,), 7.0, dtype=torch.float32, device="cuda")
+        print("case dequantize_dev %s, %d blocks" % (NAMES[typ], nblk), flush=True)
+        got = gq.gpuq_dequantize_dev(typ, d_q.data_ptr(), d_out.data_ptr(), nblk, st)
+        torch.cuda.synchronize()
+        assert got == nblk * 256 * 4
+        out = d_out.cpu().numpy()
+        assert np.array_equal(out[: nblk * 256].view(np.uint32), want.view(np.uint32)), nblk
+        assert (out[nblk * 256:] == 7.0).all(), nblk
+
+
+@pytest.mark.parametrize("src", [BF16, MXFP4], ids=["bf16", "mxfp4"])
+def test_dequantize_src_dev_ragged_counts(env, oracle_lib, src):
+    """value counts of 1, 65, 257 and 300 32-value blocks (a wave decodes 64): bit for bit, nothing written past n"""
+    torch, gq = env
+    rng = np.random.default_rng(src + 3)
+    x = (rng.standard_normal((1, 1, 32 * 300)) * 0.05).astype(np.float32)
+    raw = np.ascontiguousarray(source(oracle_lib, src, x, seed=4))
+    d_raw = torch.from_numpy(raw).cuda()
+    st = torch.cuda.current_stream().cuda_stream
+    for nb in (1, 65, 257, 300):
+        n = nb * 32
+        nbytes = n * 2 if src == BF16 else nb * 17
+        want = oracle_lib.decode_src(src, np.ascontiguousarray(raw[:nbytes]), n)
+        d_out = torch.full((n + GUARD,), 7.0, dtype=torch.float32, device="cuda")
+        print("case dequantize_src_dev src %d, %d values" % (src, n), flush=True)
+        got = gq.gpuq_dequantize_src_dev(src, d_raw.data_ptr(), d_out.data_ptr(), n, st)
+        torch.cuda.synchronize()
+        assert got == n * 4
+        out = d_out.cpu().numpy()
+        assert np.array_equal(out[:n].view(np.uint32), want.view(np.uint32)), n
+        assert (out[n:] == 7.0).all(), n
+
+
 def test_device_api_argument_checks(env):
     """calls the library refuses answer 0 and launch nothing"""
     torch, gq = env
