@@ -74,8 +74,8 @@ DEV void iq1_group_points2(bool live, const int (&m)[2], const float *x0, const 
 #pragma unroll
         for (int i = 0; i < 8; ++i) neg = neg || (srch && wk[i] < 0.f);
     }
-    if (__ballot(neg)) coop_search_m<2, 4, true>(cnt, off, ssc, p.neigh, p.neigh_len, ws, EvalIq1{grid}, g);
-    else coop_search_m<2, 4, false>(cnt, off, ssc, p.neigh, p.neigh_len, ws, EvalIq1{grid}, g);
+    if (__ballot(neg)) coop_search_m<2, 4, true, true>(cnt, off, ssc, p.neigh, p.neigh_len, ws, EvalIq1{grid}, g);
+    else coop_search_m<2, 4, false, true>(cnt, off, ssc, p.neigh, p.neigh_len, ws, EvalIq1{grid}, g);
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
         gi[k] = 0;
