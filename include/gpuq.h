@@ -74,10 +74,12 @@ size_t gpuq_quantize_dev(int type, const float *d_x, void *d_dst, int64_t nblock
  * reference's set), and the k-quants Q2_K..Q6_K (an addition: the reference reads them back through ggml) */
 int gpuq_can_dequantize_type(int type);
 
-/* gpuq/gpuq.hip:2302 gpuq_dequantize_dev: nblocks blocks (device) -> nblocks*256 f32 (device), ggml's to_float */
+/* gpuq/gpuq.hip:2302 gpuq_dequantize_dev: nblocks blocks (device) -> nblocks*256 f32 (device), ggml's to_float.
+ * d_out 16-byte aligned, d_q 2-byte aligned (0 returned before any launch otherwise). */
 size_t gpuq_dequantize_dev(int type, const void *d_q, float *d_out, int64_t nblocks, void *stream);
 
-/* gpuq/gpuq.hip:2323 gpuq_dequantize_src_dev: n values (n % 32 == 0) of F32/F16/BF16/Q8_0/MXFP4 bytes -> f32 */
+/* gpuq/gpuq.hip:2323 gpuq_dequantize_src_dev: n values (n % 32 == 0) of F32/F16/BF16/Q8_0/MXFP4 bytes -> f32.
+ * d_out 16-byte aligned; d_raw 16-byte aligned for F32 / F16 / BF16, 2-byte for Q8_0 (0 returned otherwise). */
 size_t gpuq_dequantize_src_dev(int src_type, const void *d_raw, float *d_out, int64_t n, void *stream);
 
 /* ---- additions (no counterpart in the reference) ---- */

@@ -152,6 +152,10 @@ def test_device_api_argument_checks(env):
     assert gq.gpuq_requantize_dev(F32, p, 12, out.data_ptr(), 0, 4, 512, im.data_ptr(), st) == 0
     assert gq.gpuq_dequantize_src_dev(F32, p, out.data_ptr(), 100, st) == 0                   # n % 32
     assert gq.gpuq_dequantize_src_dev(7, p, out.data_ptr(), 64, st) == 0                      # unknown source
+    assert gq.gpuq_dequantize_src_dev(F32, p, out.data_ptr() + 4, 64, st) == 0               # unaligned output
+    assert gq.gpuq_dequantize_src_dev(BF16, p + 2, out.data_ptr(), 64, st) == 0              # unaligned source
+    assert gq.gpuq_dequantize_dev(12, p, out.data_ptr() + 4, 1, st) == 0                     # unaligned output
+    assert gq.gpuq_dequantize_dev(12, p + 1, out.data_ptr(), 1, st) == 0                     # odd block address
     torch.cuda.synchronize()
     assert gq.gpuq_take_error() == 0
 
