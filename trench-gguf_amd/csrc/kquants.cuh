@@ -896,8 +896,16 @@ DEV int iq4_index(float x, const Iq4Ent *tab, float &q) {
 // and below kv[0] the first interval's ends); the nearer end by the same test x - lo < hi - x, which for equal ends
 // gives that end.
 constexpr int IQ4_Q0 = -135, IQ4_QN = 134 - IQ4_Q0 + 1;
+// (int)floorf(x) in one instruction (v_floor_f32 and v_cvt_i32_f32 are two four-clock ones) for finite x in the
+// int range. A subnormal x floors to -1 or 0, depending on the denormal mode: both index the interval [-10, 1) of
+// the codebook, so the value is the same either way.
+DEV int floor_i32(float x) {
+    int r;
+    asm("v_cvt_flr_i32_f32 %0, %1" : "=v"(r) : "v"(x));
+    return r;
+}
 DEV float iq4_value(float x, const float2 *tq) {
-    const float2 e = tq[(int)floorf(x) - IQ4_Q0];
+    const float2 e = tq[floor_i32(x) - IQ4_Q0];
     return x - e.x < e.y - x ? e.x : e.y;
 }
 // the tables (and the 16 codebook values before them), staged by a workgroup's threads
