@@ -1233,12 +1233,12 @@ static const int8_t k_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 
 /* index of the nearest codebook value, the lower one on ties away from it (gpuq/gpuq.hip:1286-1295) */
 static int nearest_iq4(float x, int value_only) {
     /* charged as the table form (the interval kv[ml] <= x < kv[ml+1] read from a table indexed by floor(x), the
-     * codebook values being integers): floor, clamp, NaN select, conversion, then the two differences, their
-     * compare and two selects; where only the value is used (the trial scales, whose |x| stays within the table for
-     * finite values) floor, conversion, the two differences, their compare and one select. The bisection below gives
-     * the same index (tests/test_iq4_table.py) */
+     * codebook values being integers): floor-and-convert (one instruction), an integer clamp, NaN select, then the
+     * two differences, their compare and two selects; where only the value is used (the trial scales, whose |x|
+     * stays within the table for finite values) floor-and-convert, the two differences, their compare and one
+     * select. The bisection below gives the same index (tests/test_iq4_table.py) */
     const int8_t *val = k_iq4nl;
-    OPS(value_only ? 6 : 9);
+    OPS(value_only ? 5 : 8);
     if (x <= val[0]) return 0;
     if (x >= val[15]) return 15;
     int lo = 0, hi = 15;
