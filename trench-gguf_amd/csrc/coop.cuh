@@ -162,6 +162,12 @@ DEV unsigned signed_key(float d) {
     return d != d ? ~0u : k;
 }
 
+// An Eval with LIST_POINTS = true reads its candidates' grid points from ev.npt, an array beside the lists with the
+// same offsets, in the same load as the list entry (no grid read a candidate); the winner's grid index is then read
+// from the list at its position, once a list.
+template <class E, class = void> struct list_points { static constexpr bool value = false; };
+template <class E> struct list_points<E, decltype((void)E::LIST_POINTS)> { static constexpr bool value = E::LIST_POINTS; };
+
 // FIRST_WAIT: wait for the first round's list entries before the rounds start. The compiler otherwise merges the
 // loop's entry (those loads pending) with its back edge and waits for each round's prefetched entries at the start
 // of that round; with the wait its waits move to the round's end. It pays for IQ1's long lists (IQ1_M 0.7% faster)
@@ -177,8 +183,17 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
     constexpr int LB = CoopWSM<M, SW, PL, NP, ES>::LB, IDM = (1 << LB) - 1;
     constexpr int SR = M / ES;                          // lists a scale row
     auto srow = [](int e) { return SR == 1 ? e : ((e >> 6) / SR) * 64 + (e & 63); };
-    // the lists through a buffer resource: 32-bit offsets, and reads past the table return 0 instead of faulting
-    const __amdgpu_buffer_rsrc_t nrs = __builtin_amdgcn_make_buffer_rsrc((void *)neigh, 0, neigh_len * 2, 0x00020000);
+    // the lists (or their points) through a buffer resource: 32-bit offsets, and reads past the table return 0
+    // instead of faulting
+    constexpr bool LP = list_points<Eval>::value;
+    const void *lbase = neigh;
+    if constexpr (LP) lbase = ev.npt;
+    const __amdgpu_buffer_rsrc_t nrs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)lbase, 0, neigh_len * (LP ? 4 : 2), 0x00020000);
+    auto entry = [&](int e) -> int {    // list element e: its grid index, or (LP) its point's bits
+        if constexpr (LP) return (int)__builtin_amdgcn_raw_buffer_load_b32(nrs, e * 4, 0, 0);
+        else return __builtin_amdgcn_raw_buffer_load_b16(nrs, e * 2, 0, 0);
+    };
     const int lane = lane_id();
     int tot = 0;
 #pragma unroll
@@ -247,7 +262,7 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
     int bpos = 0, bidx = 0;
     int idx[CH];
 #pragma unroll
-    for (int r = 0; r < CH; ++r) idx[r] = __builtin_amdgcn_raw_buffer_load_b16(nrs, (ol + (j << CSH) + r) * 2, 0, 0);
+    for (int r = 0; r < CH; ++r) idx[r] = entry(ol + (j << CSH) + r);
     if (FIRST_WAIT) __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0), expcnt and lgkmcnt unconstrained
     for (int rd = 0; rd < R; ++rd) {
         // the next piece: the list's next, or the next list's first; its list entries read now
@@ -264,7 +279,7 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
         if (rd + 1 < R) {                               // (wave-uniform)
 #pragma unroll
             for (int r = 0; r < CH; ++r)
-                idx2[r] = __builtin_amdgcn_raw_buffer_load_b16(nrs, (ol2 + (j2 << CSH) + r) * 2, 0, 0);
+                idx2[r] = entry(ol2 + (j2 << CSH) + r);
         }
         // a new list: merge the minimum of the last one, read the owner's values and scale
         if (o != cur) {
@@ -281,7 +296,8 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
 #pragma unroll
         for (int r = 0; r < CH; ++r) {
             v[r] = pv && (j << CSH) + r < ocnt;
-            pt[r] = ev.point(v[r] ? idx[r] : 0);        // (a masked position reads point 0)
+            if constexpr (LP) pt[r] = (decltype(ev.point(0)))(unsigned)idx[r];   // (a masked position: any point)
+            else pt[r] = ev.point(v[r] ? idx[r] : 0);   // (a masked position reads point 0)
         }
 #pragma unroll
         for (int r = 0; r < CH; ++r) {
@@ -291,7 +307,7 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
             const bool lt = b < bbits;                  // (selects, not a branch)
             bbits = lt ? b : bbits;
             bpos = lt ? pos : bpos;
-            bidx = lt ? idx[r] : bidx;
+            if constexpr (!LP) bidx = lt ? idx[r] : bidx;
         }
         o = o2; j = j2; ocnt = ocnt2; ol = ol2; nx = nx2;
 #pragma unroll
@@ -305,7 +321,10 @@ DEV void coop_search_m(const int (&cnt)[M], const int (&off)[M], const float (&s
     for (int m = 0; m < M; ++m) {
         if (cnt[m] > 0) {
             const unsigned long long k = ws.key[m * 64 + lane];
-            gi[m] = (unsigned)(k >> 32) >= KMAX ? -1 : (int)(k & 0xfffu);
+            if constexpr (LP)   // the winner's index from the list, at its position
+                gi[m] = (unsigned)(k >> 32) >= KMAX ? -1 : (int)neigh[off[m] + 1 + (int)((k >> 12) & 0xfffffu)];
+            else
+                gi[m] = (unsigned)(k >> 32) >= KMAX ? -1 : (int)(k & 0xfffu);
         }
     }
 }

@@ -29,6 +29,7 @@ struct QParams {
     const uint64_t *grid;
     const int32_t *map;
     const uint16_t *neigh;
+    const uint32_t *npt;    // the 4-value types: neigh's entries as grid points (same offsets; counts read 0)
     const int32_t *map3;
     int grid_size, map_size, neigh_len;
     int *err;               // set when a search finds no candidate (the reference traps there)

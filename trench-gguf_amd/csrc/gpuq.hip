@@ -65,6 +65,7 @@ struct Tabs {
     int32_t *map = nullptr;     // full key map (2-bit keys, 43692; 3-bit keys, 4096)
     int32_t *map3 = nullptr;    // the staged map, off-grid entries packed: base-3 keys (6561) or 3-bit keys (4096)
     uint16_t *neigh = nullptr;
+    uint32_t *npt = nullptr;    // the 4-value types: each list entry's grid point, beside neigh (same offsets)
     int grid_size = 0, map_size = 0, neigh_len = 0;
     uint64_t *dq = nullptr;     // dequantizer grid (record 1000 + type)
     int dq_size = 0;
@@ -367,6 +368,7 @@ QParams params_for(int type, const void *src, void *dst, int64_t nunits, const f
     p.grid = t.grid;
     p.map = t.map;
     p.neigh = t.neigh;
+    p.npt = t.npt;
     p.map3 = t.map3;
     p.grid_size = t.grid_size;
     p.map_size = t.map_size;
@@ -712,7 +714,7 @@ extern "C" int gpuq_init(const char *tables, int device) {
     // the tables of an earlier call are replaced but stay allocated until the process ends: launches still in flight
     // and graphs captured before this call keep the old pointers in their parameters and go on reading them
     for (Tabs &t : g_tabs) {
-        for (void *p : {(void *)t.grid, (void *)t.map, (void *)t.map3, (void *)t.neigh, (void *)t.dq})
+        for (void *p : {(void *)t.grid, (void *)t.map, (void *)t.map3, (void *)t.neigh, (void *)t.npt, (void *)t.dq})
             if (p) g_retired.push_back(p);
         t = Tabs();
     }
@@ -731,6 +733,12 @@ extern "C" int gpuq_init(const char *tables, int device) {
             if (!upload(&t.grid, r.grid) || !upload(&t.map, r.map) || !upload(&t.neigh, r.nb) ||
                 !upload(&t.map3, r.m3))
                 return 4;
+            if (!eight_values(r.type)) {    // the lists' points (the searches read them with the list entries)
+                std::vector<uint32_t> npt(r.nb.size(), 0u);
+                for (size_t off = 0; off < r.nb.size(); off += 1 + (size_t)r.nb[off])
+                    for (size_t j = 1; j <= r.nb[off]; ++j) npt[off + j] = (uint32_t)r.grid[r.nb[off + j]];
+                if (!upload(&t.npt, npt)) return 4;
+            }
             t.grid_size = (int)r.grid.size();
             t.map_size = (int)r.map.size();
             t.neigh_len = (int)r.nb.size();

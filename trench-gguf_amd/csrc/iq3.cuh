@@ -51,6 +51,8 @@ DEV int key3_of_point(uint32_t pt) {
 // (st[0..3] the x's, st[4..7] the weights), in the serial scan's operation order
 struct EvalIq4 {
     const uint32_t *grid;
+    const uint32_t *npt;                            // the lists' points (QParams::npt)
+    static constexpr bool LIST_POINTS = true;
     DEV uint32_t point(int idx) const { return grid[idx]; }
     DEV float operator()(const float *st, float scale, uint32_t pt) const {
         float d2 = 0;
@@ -100,7 +102,7 @@ DEV void iq3_points(const bool (&act)[8], float id, float scale, const float (&x
             sc[m] = scale;
             if (srch) coop_stage<4>(ws, xval + 4 * k, waux + 4 * k, m * 64 + lane_id());
         }
-        coop_search_m<4, IQ3_CH>(cnt, off, sc, p.neigh, p.neigh_len, ws, EvalIq4{grid}, gi);
+        coop_search_m<4, IQ3_CH>(cnt, off, sc, p.neigh, p.neigh_len, ws, EvalIq4{grid, p.npt}, gi);
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             const int k = 4 * h + m;
@@ -143,7 +145,7 @@ DEV void iq3_points2(bool live, const float (&id)[2], const float (&scale)[2], b
 #pragma unroll
         for (int m = 0; m < 4; ++m)
             coop_stage<4>(ws, xval + 4 * (4 * h + m), waux + 4 * (4 * h + m), m * 64 + lane_id());
-        coop_search_m<8, IQ3_CH>(cnt, off, sc, p.neigh, p.neigh_len, ws, EvalIq4{grid}, gi);
+        coop_search_m<8, IQ3_CH>(cnt, off, sc, p.neigh, p.neigh_len, ws, EvalIq4{grid, p.npt}, gi);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int t = e >> 2, k = 4 * h + (e & 3);
